@@ -1,0 +1,95 @@
+"""Oracle: MLX-affine 8-bit weight-only linear (group 64), restated in numpy.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Reference arithmetic restated here (paths relative to the reference repo):
+  mlx_esmc.py:43          GROUP = 64.
+  mlx_esmc.py:53-75       weights keep torch's [out, in] layout; groups of 64 run along
+                          ``in`` (K); scales and biases are stored fp16.
+  mlx_esmc.py:78-81       y = mx.quantized_matmul(x, w, s, b, transpose=True,
+                          group_size=64, bits=8) = x @ W_hat^T with
+                          W_hat[n, k] = s[n, k // 64] * q[n, k] + b[n, k // 64].
+  (mlx 0.32.3 is the third-party library holding quantized_matmul; it is not in
+   this container. Its published affine scheme is the formula above; the 8-bit
+   codes are packed four per uint32, little-endian, i.e. byte-identical to a
+   row-major uint8 [N, K] array, which is the layout used here.)
+
+Pinned by (tests/test_oracle_q8.py):
+  * exactness argument: s*q is exact in fp32 and fp64 (11 + 8 significant bits) and
+    the fp64 sum s*q + b is exact at these magnitudes, so dequant_exact is the real
+    number s*q + b, and dequant_f16 / dequant_f32 are its single roundings. Checked
+    against fractions.Fraction arithmetic on random codes;
+  * special cases: q = 0 gives b, s = 0 gives b, q = 255 with b = 0 gives s*255;
+  * the GEMM against a pure-Python loop on tiny shapes, and against the
+    dequantise-then-matmul identity y = sum_g s_g (x_g . q_g) + b_g sum(x_g).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+GROUP = 64  # mlx_esmc.py:43
+
+
+def dequant_exact(q: np.ndarray, s: np.ndarray, b: np.ndarray, group: int = GROUP) -> np.ndarray:
+    """W_hat = s*q + b per group of ``group`` along K, in fp64 (exact for fp16 s, b and uint8 q)."""
+    N, K = q.shape
+    assert K % group == 0 and s.shape == (N, K // group) and b.shape == s.shape
+    s64 = np.repeat(s.astype(np.float64), group, axis=1)
+    b64 = np.repeat(b.astype(np.float64), group, axis=1)
+    return s64 * q.astype(np.float64) + b64
+
+
+def dequant_f16(q, s, b, group: int = GROUP) -> np.ndarray:
+    """RN_fp16(s*q + b): one rounding of the exact value (what an fp16 FMA gives)."""
+    return dequant_exact(q, s, b, group).astype(np.float16)
+
+
+def dequant_f32(q, s, b, group: int = GROUP) -> np.ndarray:
+    """RN_fp32(s*q + b): one rounding; identical with or without FMA since s*q is exact in fp32."""
+    return dequant_exact(q, s, b, group).astype(np.float32)
+
+
+def q8_linear(x: np.ndarray, q, s, b, group: int = GROUP, weights: str = "exact") -> np.ndarray:
+    """y = x @ W_hat^T in fp64 (mlx_esmc.py:78-81). ``weights``: 'exact' or 'f16' (W_hat rounded to fp16)."""
+    W = dequant_exact(q, s, b, group) if weights == "exact" else dequant_f16(q, s, b, group).astype(np.float64)
+    return x.astype(np.float64) @ W.T
+
+
+def q8_linear_grouped(x: np.ndarray, q, s, b, group: int = GROUP) -> np.ndarray:
+    """Same value by the factored identity y[m,n] = sum_g s[n,g] (x_g . q_g) + b[n,g] sum(x_g)."""
+    M, K = x.shape
+    N = q.shape[0]
+    G = K // group
+    xg = x.astype(np.float64).reshape(M, G, group)
+    qg = q.astype(np.float64).reshape(N, G, group)
+    dots = np.einsum("mgk,ngk->mng", xg, qg)
+    sums = xg.sum(-1)  # [M, G]
+    return (dots * s.astype(np.float64)[None]).sum(-1) + sums @ b.astype(np.float64).T
+
+
+def q8_linear_bruteforce(x, q, s, b, group: int = GROUP):
+    """Pure-Python loop (tiny shapes only)."""
+    M, K = x.shape
+    N = q.shape[0]
+    y = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            acc = 0.0
+            for k in range(K):
+                w = float(s[n, k // group]) * int(q[n, k]) + float(b[n, k // group])
+                acc += float(x[m, k]) * w
+            y[m, n] = acc
+    return y
+
+
+def make_q8_inputs(M: int, K: int, N: int, seed: int = 0, group: int = GROUP):
+    """Seeded q8-linear inputs: x [M,K] fp16 ~ N(0,1); q [N,K] uint8 ~ U{0..255};
+    s [N,K/g] fp16 ~ U(0.001, 0.01); b [N,K/g] fp16 ~ N(0, 0.1). Drawn in that order."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g, dtype=torch.float32).half()
+    q = torch.randint(0, 256, (N, K), generator=g, dtype=torch.int64).to(torch.uint8)
+    s = (torch.rand(N, K // group, generator=g, dtype=torch.float32) * 0.009 + 0.001).half()
+    b = (torch.randn(N, K // group, generator=g, dtype=torch.float32) * 0.1).half()
+    return x.numpy(), q.numpy(), s.numpy(), b.numpy()

@@ -1,0 +1,58 @@
+"""Pins the transition / block-stack oracle (oracle/transition.py)."""
+
+import math
+
+import torch
+
+from oracle import tmu, transition as tr
+
+D = torch.float64
+
+
+def test_relu_mlp_matches_transformers_residue_mlp():
+    from transformers.models.esm.modeling_esmfold import EsmFoldResidueMLP
+    g = torch.Generator().manual_seed(0)
+    p = tr.draw_transition(g, 16, 64)
+    p.ln_w = 1 + 0.2 * torch.randn(16, generator=g)
+    p.ln_b = 0.2 * torch.randn(16, generator=g)
+    p.b1 = 0.1 * torch.randn(64, generator=g)
+    p.b3 = 0.1 * torch.randn(16, generator=g)
+    m = EsmFoldResidueMLP(16, 64).double().eval()
+    with torch.no_grad():
+        m.mlp[0].weight.copy_(p.ln_w); m.mlp[0].bias.copy_(p.ln_b)
+        m.mlp[1].weight.copy_(p.w1); m.mlp[1].bias.copy_(p.b1)
+        m.mlp[3].weight.copy_(p.w3); m.mlp[3].bias.copy_(p.b3)
+        z = torch.randn(1, 5, 5, 16, generator=g, dtype=D)
+        pd = tr.TransitionWeights(*(t.double() for t in (p.ln_w, p.ln_b, p.w1, p.w3)), b1=p.b1.double(),
+                                  b3=p.b3.double())
+        torch.testing.assert_close(tr.transition(z, pd), m(z), rtol=1e-12, atol=1e-12)
+
+
+def test_swiglu_closed_form():
+    g = torch.Generator().manual_seed(1)
+    C, H = 4, 6
+    p = tr.TransitionWeights(torch.ones(C, dtype=D), torch.zeros(C, dtype=D),
+                             torch.randn(H, C, generator=g, dtype=D), torch.randn(C, H, generator=g, dtype=D),
+                             w2=torch.randn(H, C, generator=g, dtype=D))
+    z = torch.randn(1, 2, 2, C, generator=g, dtype=D)
+    out = tr.transition(z, p)
+    h = tmu.layer_norm(z, p.ln_w, p.ln_b, p.eps)[0, 1, 0]
+    u1, u2 = p.w1 @ h, p.w2 @ h
+    act = torch.tensor([float(a) / (1 + math.exp(-float(a))) * float(bb) for a, bb in zip(u1, u2)], dtype=D)
+    torch.testing.assert_close(out[0, 1, 0], z[0, 1, 0] + p.w3 @ act, rtol=1e-12, atol=1e-12)
+
+
+def test_block_order():
+    g = torch.Generator().manual_seed(2)
+    blk = tr.draw_blocks(g, 1, 8, 8, 32)[0]
+    blk = tr.BlockWeights(blk.tri_out.to(D), blk.tri_in.to(D),
+                          tr.TransitionWeights(blk.trans.ln_w.double(), blk.trans.ln_b.double(),
+                                               blk.trans.w1.double(), blk.trans.w3.double()))
+    z = torch.randn(1, 5, 5, 8, generator=g, dtype=D)
+    z1 = z + tmu.trimul(z, None, blk.tri_out, True)
+    z2 = z1 + tmu.trimul(z1, None, blk.tri_in, False)
+    torch.testing.assert_close(tr.block_forward(z, None, blk), tr.transition(z2, blk.trans))
+    # in-then-out is a different function: the order is observable
+    z1b = z + tmu.trimul(z, None, blk.tri_in, False)
+    z2b = z1b + tmu.trimul(z1b, None, blk.tri_out, True)
+    assert not torch.allclose(z2, z2b)
