@@ -1,0 +1,241 @@
+"""Benchmark: triangle multiplicative update pair cells/s at L=238, fp16, on one MI355X.
+
+A step is one TMU pair on the pair tensor z [1, 238, 238, 128] fp16:
+z1 = z + T_out(z), z2 = z1 + T_in(z1): six kernels (a, b, c per direction), inputs
+resident in HBM. value = L^2 / t_step (cells/s).
+
+Also reported on the same JSON line:
+  roofline      for the kernel with the largest share of the step (achieved =
+                algorithmic bytes or flops per launch / its mean duration, measured
+                with HIP events on the launch stream inside the timed region);
+  kernels       the same figures for every kernel of the step;
+  q8            the 8-bit ESMC-style linears [238,2560]x[2560->10240] and
+                [238,10240]x[10240->2560] (time, TFLOP/s, GB/s);
+  cpu_baseline  the CPU oracle (torch fp32 restatement of the reference's
+                _trimul_forward) on the host cores, a bounded sample of the same
+                workload (rank 0, N=1 only).
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--graph]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+MFMA_F16_PEAK = 2.5e15     # FLOP/s, dense fp16/bf16 MFMA
+
+L, C, CL = 238, 128, 128
+
+
+def alg_counts(L: int, C: int, c: int):
+    """Algorithmic FLOPs and compulsory fp16 bytes per launch of each kernel (one direction)."""
+    N = L * L
+    return {
+        "project": {"flops": 2 * N * C * 4 * c, "bytes": 2 * N * C + 2 * 2 * c * N},
+        "contract": {"flops": 2 * c * L ** 3, "bytes": 2 * 2 * c * N + 2 * c * N},
+        "epilogue": {"flops": 2 * N * (c * C + C * C), "bytes": 2 * c * N + 2 * N * C + 2 * N * C},
+    }
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-q8", action="store_true", help="skip the q8 linear figures")
+    ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
+    return ap.parse_args()
+
+
+def cpu_baseline(z, po, pi):
+    """The CPU oracle in fp32 on the host cores: 1 warm-up, median of 3 TMU pairs at L=238."""
+    import torch
+    from oracle import tmu
+    threads = torch.get_num_threads()
+    zf = z.float()
+    with torch.no_grad():
+        tmu.trimul_pair(zf, None, po, pi)
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            tmu.trimul_pair(zf, None, po, pi)
+            ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    return {"value": L * L / t, "unit": "cells/s", "cores": threads, "kind": "port",
+            "sample": f"TMU pair (out+in, residuals) at L={L}, C=c={C}, fp32 torch on CPU, median of 3 after 1 "
+                      f"warm-up, {t * 1e3:.1f} ms per pair"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        sys.exit(2)
+    import torch
+    from __graft_entry__ import load_package
+    pkg = load_package()
+    from oracle import tmu, q8 as oq8
+
+    lib = pkg.capi.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    z, _, po, pi = tmu.make_pair_inputs(L, C, CL, seed=0, dtype=torch.float16)
+    t_out = pkg.trimul.TriMul.from_weights(po, device=dev)
+    t_in = pkg.trimul.TriMul.from_weights(pi, device=dev)
+    K = pkg.kernels
+    ld = K.leading_dim(L)
+    z0 = z.to(dev)
+    zbuf = z0.clone()
+    a = torch.empty(1, CL, L, ld, dtype=torch.float16, device=dev)
+    b = torch.empty_like(a)
+    x = torch.empty_like(a)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    scale = 1.0 / 256.0
+
+    def launch(kind, m: "pkg.trimul.TriMul", zin, zout):
+        if kind == "project":
+            rc = lib.tmu_project(zin.data_ptr(), None, m.ln_in_w.data_ptr(), m.ln_in_b.data_ptr(), m.ln_in_eps,
+                                 m.w_bundle.data_ptr(), a.data_ptr(), b.data_ptr(), 1, L, C, CL, ld,
+                                 int(not m.outgoing), sp)
+        elif kind == "contract":
+            rc = lib.tmu_contract(a.data_ptr(), b.data_ptr(), x.data_ptr(), CL, L, ld, ld, scale, sp)
+        else:
+            rc = lib.tmu_epilogue(x.data_ptr(), ld, zin.data_ptr(), None, m.ln_in_w.data_ptr(), m.ln_in_b.data_ptr(),
+                                  m.ln_in_eps, m.ln_mix_w.data_ptr(), m.ln_mix_b.data_ptr(),
+                                  m.ln_mix_eps * scale * scale, m.w_emit.data_ptr(), m.w_gate.data_ptr(),
+                                  zout.data_ptr(), 1, L, C, CL, 1, 0, sp)
+        pkg.capi.check(rc)
+
+    kinds = ("project", "contract", "epilogue")
+
+    def step(events=None):
+        # z1 = z + T_out(z) written into zbuf; z2 = z1 + T_in(z1) in place
+        for d, m in enumerate((t_out, t_in)):
+            src = z0 if d == 0 else zbuf
+            for kind in kinds:
+                if events is not None:
+                    events[(d, kind)][0].record(stream)
+                launch(kind, m, src, zbuf)
+                if events is not None:
+                    events[(d, kind)][1].record(stream)
+
+    # correctness guard on the benchmarked configuration (cheap: one pair vs the fp32 oracle)
+    step()
+    torch.cuda.synchronize()
+    got = zbuf.double().cpu() - z.double()
+    with torch.no_grad():
+        ref = tmu.trimul_pair(z.float(), None, po, pi).double() - z.double()
+    rel_err = float((got - ref).abs().max() / ref.pow(2).mean().sqrt())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    graph = None
+    if args.graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        graph.replay()
+        torch.cuda.synchronize()
+
+    # timed region: exactly `steps` steps between synchronisations
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(args.steps):
+        if graph is not None:
+            graph.replay()
+        else:
+            step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+
+    # per-kernel durations: HIP events around every launch, over a second timed pass
+    ev = {(d, k): [[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+                   for _ in range(args.steps)] for d in range(2) for k in kinds}
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        step({key: ev[key][i] for key in ev})
+    torch.cuda.synchronize()
+    counts = alg_counts(L, C, CL)
+    kern = {}
+    for k in kinds:
+        durs = [e0.elapsed_time(e1) * 1e-3 for d in range(2) for (e0, e1) in ev[(d, k)]]
+        t = statistics.mean(durs)
+        kern[k] = {"us": t * 1e6, "tflops": counts[k]["flops"] / t / 1e12,
+                   "gbs": counts[k]["bytes"] / t / 1e9,
+                   "mfma_frac": counts[k]["flops"] / t / MFMA_F16_PEAK,
+                   "hbm_frac": counts[k]["bytes"] / t / HBM_PEAK}
+    dom = max(kinds, key=lambda k: kern[k]["us"])
+    if dom == "contract":
+        roof = {"bound": "mfma", "achieved": kern[dom]["tflops"], "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
+                "frac": kern[dom]["mfma_frac"], "traffic": None, "kernel": "tmu_contract_kernel",
+                "per_launch": f"{counts[dom]['flops'] / 1e9:.3f} GFLOP"}
+    else:
+        roof = {"bound": "hbm", "achieved": kern[dom]["gbs"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": kern[dom]["hbm_frac"], "traffic": None, "kernel": f"tmu_{dom}_kernel",
+                "per_launch": f"{counts[dom]['bytes'] / 1e6:.2f} MB"}
+
+    pair_flops = 2 * sum(v["flops"] for v in counts.values())
+    pair_bytes = 2 * sum(v["bytes"] for v in counts.values())
+    out = {
+        "metric": "tri-mul-update pair cells/sec at L=238 fp16 (+% MFMA peak, % HBM BW)",
+        "value": L * L / (ms * 1e-3), "unit": "cells/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) pair tensor, N(0,1/fan_in) weights)",
+        "config": {"workload": "TMU pair outgoing+incoming with residuals, z [1,238,238,128] fp16, c_hidden 128, "
+                               "all-ones mask", "L": L, "C": C, "c_hidden": CL, "batch": 1,
+                   "launch": "hip graph" if graph is not None else "eager"},
+        "pair_mfma_frac": pair_flops / (ms * 1e-3) / MFMA_F16_PEAK,
+        "pair_hbm_frac": pair_bytes / (ms * 1e-3) / HBM_PEAK,
+        "max_err_over_rms": rel_err,
+        "roofline": roof,
+        "kernels": kern,
+    }
+
+    if not args.no_q8:
+        qres = {}
+        for (Kd, Nd) in ((2560, 10240), (10240, 2560)):
+            xq, qq, sq, bq = oq8.make_q8_inputs(L, Kd, Nd, seed=Kd)
+            xt, qt = torch.from_numpy(xq).to(dev), torch.from_numpy(qq).to(dev)
+            st, bt = torch.from_numpy(sq).to(dev), torch.from_numpy(bq).to(dev)
+            y = torch.empty(L, Nd, dtype=torch.float16, device=dev)
+            for _ in range(5):
+                K.q8_linear(xt, qt, st, bt, out=y)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            reps = 50
+            for _ in range(reps):
+                K.q8_linear(xt, qt, st, bt, out=y)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) * 1e-3 / reps
+            fl = 2 * L * Kd * Nd
+            by = Nd * Kd + 2 * 2 * Nd * (Kd // 64) + 2 * L * Kd + 2 * L * Nd
+            qres[f"{L}x{Kd}->{Nd}"] = {"us": t * 1e6, "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
+                                      "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK}
+        out["q8"] = qres
+
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(z, po, pi)
+        out["speedup_vs_cpu"] = out["value"] / out["cpu_baseline"]["value"]
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,1 +1,23 @@
-"""placeholder"""
+"""esmfold2-mlx_amd: ESMFold2's triangle multiplicative update and 8-bit ESMC linear
+as hand-written gfx950 (MI355X) HIP kernels behind a C ABI (include/esmfold2_amd.h).
+
+Modules:
+  build            -- compile libesmfold2_amd.so in-tree with hipcc (gfx950)
+  capi             -- ctypes binding of the C ABI; raises, never falls back
+  kernels          -- one functional wrapper per C entry point (torch tensors in/out)
+  trimul           -- TriMul / TriMulPair: the forward(pair_grid, visibility) module contract
+  q8               -- Q8Linear: the quantized_matmul(transpose=True, group 64, bits 8) contract
+  var_hip_trimul   -- the reference-style variant plugin: apply(model)
+  smoke            -- one tiny GPU run checked against the CPU oracle
+"""
+
+from . import build, capi  # noqa: F401
+
+__all__ = ["build", "capi", "kernels", "trimul", "q8", "var_hip_trimul", "smoke"]
+
+
+def __getattr__(name):
+    if name in ("kernels", "trimul", "q8", "var_hip_trimul", "smoke"):
+        import importlib
+        return importlib.import_module(f"{__name__}.{name}")
+    raise AttributeError(name)

@@ -1,0 +1,79 @@
+"""ctypes binding of libesmfold2_amd.so (the C ABI declared in include/esmfold2_amd.h).
+
+There is no fallback: if the library is missing, fails to load, or no GPU is
+present when one is required, this raises. Every wrapper checks the return code
+and raises ``EsmError`` with the library's message.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from . import build as _build
+
+_vp, _int, _f32, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/esmfold2_amd.h
+SIGNATURES = {
+    "esm_last_error": (ctypes.c_char_p, []),
+    "esm_version": (ctypes.c_char_p, []),
+    "tmu_workspace_bytes": (_sz, [_int, _int, _int]),
+    "tmu_leading_dim": (_int, [_int]),
+    "tmu_project": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp]),
+    "tmu_contract": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _f32, _vp]),
+    "tmu_epilogue": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int,
+                            _int, _int, _int, _vp]),
+    "tmu_forward": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _int, _int, _int,
+                           _int, _int, _int, _int, _vp]),
+    "q8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
+    "q8_dequant": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
+}
+
+ERRORS = {-1: "ESM_ERR_NULL", -2: "ESM_ERR_SHAPE", -3: "ESM_ERR_ALIGN", -4: "ESM_ERR_UNSUPPORTED",
+          -5: "ESM_ERR_DEVICE"}
+
+
+class EsmError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{ERRORS.get(code, f'hipError {code}')}] {msg}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib_path() -> str:
+    return _build.LIB_PATH
+
+
+def lib(reload: bool = False, require_gpu: bool = True) -> ctypes.CDLL:
+    """The loaded library. Builds it only if no built library exists."""
+    global _lib
+    with _lock:
+        if _lib is None or reload:
+            if not os.path.exists(_build.LIB_PATH):
+                _build.build(force=True)
+            handle = ctypes.CDLL(_build.LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)  # AttributeError if a declared symbol is missing
+                fn.restype, fn.argtypes = res, args
+            _lib = handle
+    if require_gpu:
+        import torch
+        if not torch.cuda.is_available():
+            raise EsmError(-5, "no ROCm GPU visible: the HIP path has no CPU fallback")
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise EsmError(rc, _lib.esm_last_error().decode())
+
+
+def stream_ptr(stream=None) -> int:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream

@@ -1,0 +1,202 @@
+// C ABI (include/esmfold2_amd.h): argument validation, launch geometry and
+// error reporting around the gfx950 kernels. Nothing here allocates device
+// memory; every launch goes on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+
+#include "../../include/esmfold2_amd.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return ESM_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail((int)e, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Compute units of the current device (persistent-grid sizing), cached per device.
+int cu_count() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+constexpr int kMaxL = 4096;  // pair side limit: keeps every 32-bit tile index in range
+
+using esm::half_t;
+inline const half_t* H(const esm_half* p) { return reinterpret_cast<const half_t*>(p); }
+inline half_t* H(esm_half* p) { return reinterpret_cast<half_t*>(p); }
+
+int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+}  // namespace
+
+extern "C" {
+
+const char* esm_last_error(void) { return g_err.c_str(); }
+
+const char* esm_version(void) { return "esmfold2_amd 0.1.0 gfx950"; }
+
+int tmu_leading_dim(int L) { return L <= 0 ? 0 : round_up(L, 8); }
+
+size_t tmu_workspace_bytes(int B, int L, int c) {
+  if (B <= 0 || L <= 0 || c <= 0) return 0;
+  const size_t plane = (size_t)B * c * L * tmu_leading_dim(L) * sizeof(esm_half);
+  const size_t a256 = (plane + 255) / 256 * 256;
+  return 3 * a256;
+}
+
+int tmu_project(const esm_half* z, const esm_half* mask, const float* ln_w, const float* ln_b, float ln_eps,
+                const esm_half* w, esm_half* a_out, esm_half* b_out, int B, int L, int C, int c, int ld,
+                int incoming, void* stream) {
+  if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_project: B=%d L=%d must be >= 0", B, L);
+  if (C != 128 || c != 128) return fail(ESM_ERR_UNSUPPORTED, "tmu_project: C=%d c=%d (supported: 128, 128)", C, c);
+  if (B == 0 || L == 0) return ok();
+  if (!z || !ln_w || !ln_b || !w || !a_out || !b_out) return fail(ESM_ERR_NULL, "tmu_project: NULL pointer");
+  if (L > kMaxL) return fail(ESM_ERR_SHAPE, "tmu_project: L=%d exceeds %d", L, kMaxL);
+  if (ld % 8 != 0 || ld < L || ld > round_up(L, esm::kCellTile))
+    return fail(ESM_ERR_SHAPE, "tmu_project: ld=%d must be a multiple of 8 in [L, roundup(L,%d)] (L=%d)", ld,
+                esm::kCellTile, L);
+  if (!aligned16(z) || !aligned16(w) || !aligned16(a_out) || !aligned16(b_out))
+    return fail(ESM_ERR_ALIGN, "tmu_project: z, w, a, b must be 16-byte aligned");
+  if (!(ln_eps >= 0.f)) return fail(ESM_ERR_SHAPE, "tmu_project: eps must be >= 0");
+  esm::ProjectArgs a{H(z), mask ? H(mask) : nullptr, ln_w, ln_b, ln_eps, H(w), H(a_out), H(b_out), B, L, ld,
+                     incoming ? 1 : 0, 0, 0};
+  a.tiles_per_line = (L + esm::kCellTile - 1) / esm::kCellTile;
+  const long long ntiles = (long long)B * L * a.tiles_per_line;
+  if (ntiles > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_project: too many tiles");
+  a.ntiles = (int)ntiles;
+  const int grid = (int)(ntiles < cu_count() ? ntiles : cu_count());
+  return hip_status(esm::launch_project(a, grid, (hipStream_t)stream), "tmu_project launch");
+}
+
+int tmu_contract(const esm_half* a, const esm_half* b, esm_half* x, int batch, int L, int ld, int ldx, float scale,
+                 void* stream) {
+  if (batch < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_contract: batch=%d L=%d must be >= 0", batch, L);
+  if (batch == 0 || L == 0) return ok();
+  if (!a || !b || !x) return fail(ESM_ERR_NULL, "tmu_contract: NULL pointer");
+  if (L > kMaxL || batch > 65535) return fail(ESM_ERR_SHAPE, "tmu_contract: L=%d batch=%d out of range", L, batch);
+  if (ld % 8 != 0 || ld < L || ldx % 8 != 0 || ldx < L)
+    return fail(ESM_ERR_SHAPE, "tmu_contract: ld=%d ldx=%d must be multiples of 8 and >= L=%d", ld, ldx, L);
+  if (!aligned16(a) || !aligned16(b) || !aligned16(x))
+    return fail(ESM_ERR_ALIGN, "tmu_contract: a, b, x must be 16-byte aligned");
+  esm::ContractArgs args{H(a), H(b), H(x), batch, L, ld, ldx, scale, (L + esm::kContractTile - 1) / esm::kContractTile};
+  return hip_status(esm::launch_contract(args, (hipStream_t)stream), "tmu_contract launch");
+}
+
+int tmu_epilogue(const esm_half* x, int ldx, const esm_half* z, const esm_half* mask, const float* ln_in_w,
+                 const float* ln_in_b, float ln_in_eps, const float* ln_mix_w, const float* ln_mix_b,
+                 float ln_mix_eps, const esm_half* w_emit, const esm_half* w_gate, esm_half* out, int B, int L,
+                 int C, int c, int residual, int out_mask, void* stream) {
+  if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_epilogue: B=%d L=%d must be >= 0", B, L);
+  if (C != 128 || c != 128) return fail(ESM_ERR_UNSUPPORTED, "tmu_epilogue: C=%d c=%d (supported: 128, 128)", C, c);
+  if (B == 0 || L == 0) return ok();
+  if (!x || !z || !ln_in_w || !ln_in_b || !ln_mix_w || !ln_mix_b || !w_emit || !w_gate || !out)
+    return fail(ESM_ERR_NULL, "tmu_epilogue: NULL pointer");
+  if (L > kMaxL) return fail(ESM_ERR_SHAPE, "tmu_epilogue: L=%d exceeds %d", L, kMaxL);
+  if (ldx % 8 != 0 || ldx < L) return fail(ESM_ERR_SHAPE, "tmu_epilogue: ldx=%d must be a multiple of 8, >= L", ldx);
+  if (!aligned16(x) || !aligned16(z) || !aligned16(w_emit) || !aligned16(w_gate) || !aligned16(out))
+    return fail(ESM_ERR_ALIGN, "tmu_epilogue: x, z, w_emit, w_gate, out must be 16-byte aligned");
+  if (out == z && !residual)
+    return fail(ESM_ERR_SHAPE, "tmu_epilogue: out may alias z only with residual=1");
+  if (out_mask && !mask) return fail(ESM_ERR_NULL, "tmu_epilogue: out_mask=1 needs a mask");
+  if (!(ln_in_eps >= 0.f) || !(ln_mix_eps >= 0.f)) return fail(ESM_ERR_SHAPE, "tmu_epilogue: eps must be >= 0");
+  esm::EpilogueArgs e{H(x), ldx, H(z), mask ? H(mask) : nullptr, ln_in_w, ln_in_b, ln_in_eps, ln_mix_w, ln_mix_b,
+                      ln_mix_eps, H(w_emit), H(w_gate), H(out), B, L, residual ? 1 : 0, out_mask ? 1 : 0, 0, 0};
+  e.tiles_per_line = (L + esm::kCellTile - 1) / esm::kCellTile;
+  const long long ntiles = (long long)B * L * e.tiles_per_line;
+  if (ntiles > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_epilogue: too many tiles");
+  e.ntiles = (int)ntiles;
+  const int per_cu = 2;
+  const long long cap = (long long)cu_count() * per_cu;
+  const int grid = (int)(ntiles < cap ? ntiles : cap);
+  return hip_status(esm::launch_epilogue(e, grid, (hipStream_t)stream), "tmu_epilogue launch");
+}
+
+int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, const float* ln_in_b, float ln_in_eps,
+                const esm_half* w_bundle, const float* ln_mix_w, const float* ln_mix_b, float ln_mix_eps,
+                const esm_half* w_emit, const esm_half* w_gate, esm_half* out, void* workspace, int B, int L, int C,
+                int c, int outgoing, int residual, int out_mask, void* stream) {
+  if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_forward: B=%d L=%d must be >= 0", B, L);
+  if (C != 128 || c != 128) return fail(ESM_ERR_UNSUPPORTED, "tmu_forward: C=%d c=%d (supported: 128, 128)", C, c);
+  if (B == 0 || L == 0) return ok();
+  if (!workspace) return fail(ESM_ERR_NULL, "tmu_forward: NULL workspace");
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(ESM_ERR_ALIGN, "tmu_forward: workspace must be 256-byte aligned");
+  const int ld = tmu_leading_dim(L);
+  const size_t plane = (size_t)B * c * L * ld;
+  const size_t a256 = (plane * sizeof(esm_half) + 255) / 256 * 256 / sizeof(esm_half);
+  esm_half* wa = static_cast<esm_half*>(workspace);
+  esm_half* wb = wa + a256;
+  esm_half* wx = wb + a256;
+  // fp16 range scheme (mlx_trunk.py:14-19): the contraction is stored as x/256
+  // and norm_mix's eps divided by 256^2; LN(x/s, eps/s^2) == LN(x, eps) exactly.
+  const float kScale = 1.0f / 256.0f;
+  int rc = tmu_project(z, mask, ln_in_w, ln_in_b, ln_in_eps, w_bundle, wa, wb, B, L, C, c, ld, outgoing ? 0 : 1,
+                       stream);
+  if (rc) return rc;
+  rc = tmu_contract(wa, wb, wx, B * c, L, ld, ld, kScale, stream);
+  if (rc) return rc;
+  return tmu_epilogue(wx, ld, z, mask, ln_in_w, ln_in_b, ln_in_eps, ln_mix_w, ln_mix_b, ln_mix_eps * kScale * kScale,
+                      w_emit, w_gate, out, B, L, C, c, residual, out_mask, stream);
+}
+
+int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* y, int M, int K,
+              int N, int group, void* stream) {
+  if (M < 0 || K < 0 || N < 0) return fail(ESM_ERR_SHAPE, "q8_linear: M=%d K=%d N=%d must be >= 0", M, K, N);
+  if (group != 64) return fail(ESM_ERR_UNSUPPORTED, "q8_linear: group=%d (supported: 64)", group);
+  if (M == 0 || N == 0) return ok();
+  if (K == 0 || K % 64 != 0 || N % 64 != 0)
+    return fail(ESM_ERR_SHAPE, "q8_linear: K=%d and N=%d must be positive multiples of 64", K, N);
+  if (!x || !q || !s || !b || !y) return fail(ESM_ERR_NULL, "q8_linear: NULL pointer");
+  if (M > 65535 * 64) return fail(ESM_ERR_SHAPE, "q8_linear: M=%d too large", M);
+  if (!aligned16(x) || !aligned16(q) || (reinterpret_cast<uintptr_t>(y) & 7u) != 0 ||
+      (reinterpret_cast<uintptr_t>(s) & 1u) != 0 || (reinterpret_cast<uintptr_t>(b) & 1u) != 0)
+    return fail(ESM_ERR_ALIGN, "q8_linear: x, q must be 16-byte aligned and y 8-byte aligned");
+  esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N};
+  return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear launch");
+}
+
+int q8_dequant(const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* w, int N, int K, int group,
+               void* stream) {
+  if (N < 0 || K < 0) return fail(ESM_ERR_SHAPE, "q8_dequant: N=%d K=%d must be >= 0", N, K);
+  if (group != 64) return fail(ESM_ERR_UNSUPPORTED, "q8_dequant: group=%d (supported: 64)", group);
+  if (N == 0 || K == 0) return ok();
+  if (K % 64 != 0) return fail(ESM_ERR_SHAPE, "q8_dequant: K=%d must be a multiple of 64", K);
+  if (!q || !s || !b || !w) return fail(ESM_ERR_NULL, "q8_dequant: NULL pointer");
+  if (!aligned16(q) || !aligned16(w)) return fail(ESM_ERR_ALIGN, "q8_dequant: q, w must be 16-byte aligned");
+  return hip_status(esm::launch_q8_dequant(q, H(s), H(b), H(w), N, K, (hipStream_t)stream), "q8_dequant launch");
+}
+
+}  // extern "C"

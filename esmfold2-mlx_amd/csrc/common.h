@@ -1,0 +1,81 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels: vector types, MFMA
+// wrappers, 16-lane LayerNorm reductions and fp16 packing.
+//
+// MFMA lane layouts used throughout (checked on an MI355X by an in-bounds
+// probe before any kernel relied on them):
+//   v_mfma_f32_32x32x16_f16(a, b, c):
+//     a: 8 halfs per lane, row  = lane % 32, k = 8*(lane/32) + e   (A is 32x16)
+//     b: 8 halfs per lane, col  = lane % 32, k = 8*(lane/32) + e   (B is 16x32)
+//     c/d: 16 floats per lane, col = lane % 32,
+//          row = 8*(r/4) + 4*(lane/32) + (r%4) for register r.
+//   A GEMM only needs A and B to agree on the k assignment, so "k = 8*(lane/32)+e"
+//   is a convention both operands follow.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define DEV __device__ __forceinline__
+
+DEV f32x16 mfma32(half8 a, half8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+DEV f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Row of the 32x32 MFMA accumulator held by register r of this lane.
+DEV int acc_row32(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+DEV half8 ld16(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
+DEV void st16(half_t* p, half8 v) { *reinterpret_cast<half8*>(p) = v; }
+
+DEV half8 zero_half8() {
+  half8 v;
+#pragma unroll
+  for (int e = 0; e < 8; e++) v[e] = (half_t)0.0f;
+  return v;
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16k .. 16k+15); every lane gets the sum.
+DEV float row16_sum(float v) {
+  v += __shfl_xor(v, 8, 16);
+  v += __shfl_xor(v, 4, 16);
+  v += __shfl_xor(v, 2, 16);
+  v += __shfl_xor(v, 1, 16);
+  return v;
+}
+
+DEV float sigmoidf_fast(float x) {
+  // 1 / (1 + e^-x): v_exp_f32 and v_rcp_f32 (about 1 ulp each); saturates
+  // cleanly to 0 and 1 at +-inf.
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
+// LayerNorm of one 8-channel slice held by this lane, where the 16 lanes of a
+// DPP row together hold one 128-channel row. Statistics in fp32, two-pass.
+DEV void ln_row128(float (&v)[8], const float (&g)[8], const float (&b)[8], float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) s += v[e];
+  const float mean = row16_sum(s) * (1.0f / 128.0f);
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    v[e] -= mean;
+    q += v[e] * v[e];
+  }
+  const float rstd = rsqrtf(row16_sum(q) * (1.0f / 128.0f) + eps);
+#pragma unroll
+  for (int e = 0; e < 8; e++) v[e] = v[e] * rstd * g[e] + b[e];
+}

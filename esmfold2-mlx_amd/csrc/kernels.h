@@ -1,0 +1,76 @@
+// Internal launch interface between the C ABI (capi.cpp) and the kernels.
+// Arguments are validated by the caller before any launcher runs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace esm {
+
+typedef _Float16 half_t;
+
+struct ProjectArgs {
+  const half_t* z;      // [B, L, L, C]
+  const half_t* mask;   // [B, L, L] or nullptr
+  const float* ln_w;    // [C]
+  const float* ln_b;    // [C]
+  float eps;
+  const half_t* w;      // [4c, C]
+  half_t* a;            // [B, c, L, ld]
+  half_t* b;            // [B, c, L, ld]
+  int B, L, ld;
+  int transpose;        // 1: store cell (r, s) at row s, column r
+  int ntiles, tiles_per_line;
+};
+
+struct ContractArgs {
+  const half_t* a;      // [batch, L, ld]
+  const half_t* b;      // [batch, L, ld]
+  half_t* x;            // [batch, L, ldx]
+  int batch, L, ld, ldx;
+  float scale;
+  int tiles;            // tiles per side: ceil(L / 128)
+};
+
+struct EpilogueArgs {
+  const half_t* x;      // [B, c, L, ldx]
+  int ldx;
+  const half_t* z;      // [B, L, L, C]
+  const half_t* mask;   // [B, L, L] or nullptr
+  const float* ln_in_w;
+  const float* ln_in_b;
+  float eps_in;
+  const float* ln_mix_w;
+  const float* ln_mix_b;
+  float eps_mix;
+  const half_t* w_emit; // [C, c]
+  const half_t* w_gate; // [C, C]
+  half_t* out;          // [B, L, L, C]
+  int B, L;
+  int residual, out_mask;
+  int ntiles, tiles_per_line;
+};
+
+struct Q8Args {
+  const half_t* x;      // [M, K]
+  const uint8_t* q;     // [N, K]
+  const half_t* s;      // [N, K/64]
+  const half_t* b;      // [N, K/64]
+  half_t* y;            // [M, N]
+  int M, K, N;
+};
+
+// Cells per tile of the per-cell kernels (a) and (c).
+constexpr int kCellTile = 64;
+// Output tile side of the contraction.
+constexpr int kContractTile = 128;
+
+// Each launcher returns the hipError_t of the launch.
+hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s);
+hipError_t launch_contract(const ContractArgs& a, hipStream_t s);
+hipError_t launch_epilogue(const EpilogueArgs& a, int grid, hipStream_t s);
+hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s);
+hipError_t launch_q8_dequant(const uint8_t* q, const half_t* s, const half_t* b, half_t* w, int N, int K,
+                             hipStream_t st);
+
+}  // namespace esm

@@ -1,0 +1,116 @@
+"""Functional wrappers of the C ABI on torch tensors (device memory and streams only).
+
+Each function checks device, dtype and contiguity, allocates its outputs with
+torch, passes raw pointers plus the current HIP stream, and raises
+``capi.EsmError`` on a non-zero return. No CPU path exists.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import capi
+
+F16 = torch.float16
+
+
+def _dev(t: torch.Tensor, name: str, dtype=None) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise capi.EsmError(-5, f"{name} must be a CUDA(HIP) tensor; the HIP path has no CPU fallback")
+    if dtype is not None and t.dtype != dtype:
+        raise capi.EsmError(-2, f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise capi.EsmError(-3, f"{name} must be contiguous")
+    return t
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def leading_dim(L: int) -> int:
+    return capi.lib().tmu_leading_dim(L)
+
+
+def workspace_bytes(B: int, L: int, c: int) -> int:
+    return capi.lib().tmu_workspace_bytes(B, L, c)
+
+
+def project(z, mask, ln_w, ln_b, eps, w, incoming: bool, ld: int | None = None):
+    """Kernel (a): -> (a, b) [B, c, L, ld] fp16 (transposed storage when ``incoming``)."""
+    lib = capi.lib()
+    _dev(z, "z", F16)
+    B, L, _, C = z.shape
+    c = w.shape[0] // 4
+    ld = lib.tmu_leading_dim(L) if ld is None else ld
+    a = torch.empty(B, c, L, ld, dtype=F16, device=z.device)
+    b = torch.empty_like(a)
+    if mask is not None:
+        _dev(mask, "mask", F16)
+    capi.check(lib.tmu_project(z.data_ptr(), _ptr(mask), _dev(ln_w, "ln_w", torch.float32).data_ptr(),
+                               _dev(ln_b, "ln_b", torch.float32).data_ptr(), float(eps), _dev(w, "w", F16).data_ptr(),
+                               a.data_ptr(), b.data_ptr(), B, L, C, c, ld, int(incoming), capi.stream_ptr()))
+    return a, b
+
+
+def contract(a, b, L: int, scale: float = 1.0, ldx: int | None = None):
+    """Kernel (b): x[n, i, j] = scale * sum_k a[n, i, k] b[n, j, k]; a, b [..., L, ld] -> x [..., L, ldx]."""
+    lib = capi.lib()
+    _dev(a, "a", F16)
+    _dev(b, "b", F16)
+    ld = a.shape[-1]
+    batch = a.numel() // (L * ld)
+    ldx = lib.tmu_leading_dim(L) if ldx is None else ldx
+    x = torch.empty(*a.shape[:-2], L, ldx, dtype=F16, device=a.device)
+    capi.check(lib.tmu_contract(a.data_ptr(), b.data_ptr(), x.data_ptr(), batch, L, ld, ldx, float(scale),
+                                capi.stream_ptr()))
+    return x
+
+
+def epilogue(x, z, mask, ln_in_w, ln_in_b, eps_in, ln_mix_w, ln_mix_b, eps_mix, w_emit, w_gate,
+             residual: bool = False, out_mask: bool = False, out=None):
+    """Kernel (c): -> update (or z + update) [B, L, L, C] fp16."""
+    lib = capi.lib()
+    _dev(x, "x", F16)
+    _dev(z, "z", F16)
+    B, L, _, C = z.shape
+    c = w_emit.shape[1]
+    out = torch.empty_like(z) if out is None else _dev(out, "out", F16)
+    if mask is not None:
+        _dev(mask, "mask", F16)
+    capi.check(lib.tmu_epilogue(x.data_ptr(), x.shape[-1], z.data_ptr(), _ptr(mask),
+                                _dev(ln_in_w, "ln_in_w", torch.float32).data_ptr(),
+                                _dev(ln_in_b, "ln_in_b", torch.float32).data_ptr(), float(eps_in),
+                                _dev(ln_mix_w, "ln_mix_w", torch.float32).data_ptr(),
+                                _dev(ln_mix_b, "ln_mix_b", torch.float32).data_ptr(), float(eps_mix),
+                                _dev(w_emit, "w_emit", F16).data_ptr(), _dev(w_gate, "w_gate", F16).data_ptr(),
+                                out.data_ptr(), B, L, C, c, int(residual), int(out_mask), capi.stream_ptr()))
+    return out
+
+
+def q8_linear(x, q, s, b, group: int = 64, out=None):
+    """Kernel (d): y = x . W^T, W = s*q + b per group of 64 along K (fp16 in/out, fp32 accumulation)."""
+    lib = capi.lib()
+    _dev(x, "x", F16)
+    _dev(q, "q", torch.uint8)
+    _dev(s, "s", F16)
+    _dev(b, "b", F16)
+    M, K = x.shape
+    N = q.shape[0]
+    if q.shape[1] != K or s.shape != (N, K // group) or b.shape != s.shape:
+        raise capi.EsmError(-2, f"q8_linear: shapes x{tuple(x.shape)} q{tuple(q.shape)} s{tuple(s.shape)}")
+    y = torch.empty(M, N, dtype=F16, device=x.device) if out is None else _dev(out, "out", F16)
+    capi.check(lib.q8_linear(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), y.data_ptr(), M, K, N, group,
+                             capi.stream_ptr()))
+    return y
+
+
+def q8_dequant(q, s, b, group: int = 64):
+    """W = RN_fp16(s*q + b) [N, K] fp16: the weights q8_linear multiplies by."""
+    lib = capi.lib()
+    _dev(q, "q", torch.uint8)
+    N, K = q.shape
+    w = torch.empty(N, K, dtype=F16, device=q.device)
+    capi.check(lib.q8_dequant(q.data_ptr(), _dev(s, "s", F16).data_ptr(), _dev(b, "b", F16).data_ptr(),
+                              w.data_ptr(), N, K, group, capi.stream_ptr()))
+    return w

@@ -1,0 +1,51 @@
+"""8-bit weight-only linear on the HIP path, the contract of the reference's ``_linear``.
+
+The reference computes ``mx.quantized_matmul(x, w, s, b, transpose=True,
+group_size=64, bits=8)`` (mlx_esmc.py:78-81) on weights quantised along the
+input axis of torch's [out, in] layout with fp16 scales and biases
+(mlx_esmc.py:53-75). ``Q8Linear`` takes the same three arrays (codes as uint8
+[N, K], which is the little-endian byte view of MLX's uint32 packing) and
+computes y = x . W^T with W = s*q + b on the gfx950 kernel: fp16 activations,
+fp32 accumulation, fp16 output.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import kernels
+
+GROUP = 64
+
+
+class Q8Linear(nn.Module):
+    def __init__(self, q: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, device=None):
+        super().__init__()
+        N, K = q.shape
+        if K % GROUP or N % 64 or tuple(scales.shape) != (N, K // GROUP) or tuple(biases.shape) != (N, K // GROUP):
+            raise ValueError(f"q8 shapes: q {tuple(q.shape)}, scales {tuple(scales.shape)}, biases {tuple(biases.shape)}")
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.register_buffer("q", q.detach().to(device=dev, dtype=torch.uint8).contiguous())
+        self.register_buffer("scales", scales.detach().to(device=dev, dtype=torch.float16).contiguous())
+        self.register_buffer("biases", biases.detach().to(device=dev, dtype=torch.float16).contiguous())
+        self.in_features, self.out_features = K, N
+
+    @classmethod
+    def from_packed_u32(cls, w_u32: torch.Tensor, scales, biases, **kw) -> "Q8Linear":
+        """From MLX's packing: [N, K/4] uint32 words, four codes each, little-endian."""
+        w = w_u32.detach().cpu().contiguous()
+        if w.dtype not in (torch.int32, torch.uint32):
+            raise ValueError("packed codes must be 32-bit words")
+        q = w.view(torch.uint8).reshape(w.shape[0], w.shape[1] * 4)
+        return cls(q, scales, biases, **kw)
+
+    def dequantized(self) -> torch.Tensor:
+        return kernels.q8_dequant(self.q, self.scales, self.biases, GROUP)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
+        y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP)
+        y = y.reshape(*lead, self.out_features)
+        return y if x.dtype == torch.float16 else y.to(x.dtype)

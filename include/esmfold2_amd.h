@@ -1,0 +1,173 @@
+/*
+ * esmfold2_amd.h -- C ABI of the MI355X (gfx950) triangle multiplicative update
+ * and 8-bit weight-only linear.
+ *
+ * One shared library, libesmfold2_amd.so, exports every function below. All
+ * pointers are device pointers owned by the caller (the library never allocates
+ * on these paths); every launch goes on the caller's HIP stream; every function
+ * validates shapes, alignment and pointers before launching anything.
+ *
+ * Return codes: 0 = success; a negative ESM_ERR_* value = the arguments were
+ * rejected before launch (nothing ran); a positive value = a hipError_t reported
+ * by the runtime. esm_last_error() gives a message for the calling thread.
+ *
+ * Element types: fp16 values are IEEE binary16 (passed as uint16_t bit patterns,
+ * esm_half); fp32 values are float; 8-bit codes are uint8_t.
+ *
+ * The interfaces these entry points replace (paths relative to the reference
+ * repository, abhi0raj/esmfold2-mlx) are cited per function. The reference's
+ * kernel-level interface is mx.fast.metal_kernel objects whose outputs MLX
+ * allocates; here the caller allocates outputs and passes them in.
+ */
+#ifndef ESMFOLD2_AMD_H
+#define ESMFOLD2_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t esm_half;
+
+#define ESM_OK 0
+#define ESM_ERR_NULL (-1)        /* a required pointer is NULL                       */
+#define ESM_ERR_SHAPE (-2)       /* a size is out of range or inconsistent           */
+#define ESM_ERR_ALIGN (-3)       /* a pointer or leading dimension is misaligned     */
+#define ESM_ERR_UNSUPPORTED (-4) /* a valid but not implemented configuration        */
+#define ESM_ERR_DEVICE (-5)      /* no usable gfx950 device                          */
+
+/* Message for the last non-zero return on this thread ("" if none). */
+const char* esm_last_error(void);
+
+/* Library version string and the device architecture it was built for. */
+const char* esm_version(void);
+
+/* Bytes of caller-provided workspace tmu_forward needs for B x L x L cells with
+ * c latent channels: two operands [B, c, L, ld] and the contraction output
+ * [B, c, L, ld], fp16, with ld = tmu_leading_dim(L). */
+size_t tmu_workspace_bytes(int B, int L, int c);
+
+/* Padded row length (elements) of the channel-major operands: L rounded up to 8,
+ * so every row starts 16-byte aligned. */
+int tmu_leading_dim(int L);
+
+/*
+ * Kernel (a): input LayerNorm -> C->4c projection -> sigmoid gates -> mask ->
+ * channel-major operands, in one pass over z.
+ *
+ * Replaces, in the reference:
+ *   mx.fast.layer_norm(z, ln_in_w, ln_in_b, EPS)   mlx_trunk_kernels.py:233 (mlx_trunk.py:81)
+ *   proj = n @ w_in                                 mlx_trunk_kernels.py:214
+ *   gate_cf(proj, mask, c) -> a, b [B, c, L, L]     mlx_trunk_kernels.py:85-97 (MSL :48-80)
+ *   fast_trunk._trimul_forward lines 22-26          fast_trunk.py:22-26
+ *
+ * z       [B, L, L, C] fp16, cell-major (the pair tensor).
+ * mask    [B, L, L] fp16 pair mask (visibility) or NULL for all ones.
+ * ln_w/b  [C] fp32 norm_start weight and bias; ln_eps its eps.
+ * w       [4c, C] fp16 proj_bundle.weight, rows [s_a | s_b | g_a | g_b], no bias.
+ * a_out,
+ * b_out   [B, c, L, ld] fp16: a = s_a*sigmoid(g_a)*m, b = s_b*sigmoid(g_b)*m.
+ *         incoming = 0: the value of cell (i, k) is stored at row i, column k.
+ *         incoming = 1: stored spatially transposed (row k, column i), so the
+ *         contraction is the same A.B^T for both directions.
+ *         Columns [L, ld) are written with zeros.
+ * Supported: C = c = 128. ld % 8 == 0, ld >= L. All pointers 16-byte aligned.
+ */
+int tmu_project(const esm_half* z, const esm_half* mask, const float* ln_w, const float* ln_b, float ln_eps,
+                const esm_half* w, esm_half* a_out, esm_half* b_out, int B, int L, int C, int c, int ld,
+                int incoming, void* stream);
+
+/*
+ * Kernel (b): the triangle contraction as an fp16 MFMA batched GEMM with fp32
+ * accumulation:  x[n, i, j] = scale * sum_k a[n, i, k] * b[n, j, k]
+ * for n in [0, batch) (batch = B*c channels), i, j in [0, L), k in [0, ld).
+ *
+ * Replaces, in the reference:
+ *   a @ b.swapaxes(2, 3)  (outgoing)                mlx_trunk_kernels.py:219, mlx_trunk.py:86-88
+ *   a.swapaxes(2, 3) @ b  (incoming; here its operands come pre-transposed from tmu_project)
+ *   self._triangular_contract(left, right)          fast_trunk.py:27-30
+ *
+ * a, b  [batch, L, ld] fp16, zero in columns [L, ld).
+ * x     [batch, L, ldx] fp16; columns [L, ldx) are written with zeros.
+ * scale fp32 factor applied to the fp32 accumulator before the one rounding to
+ *       fp16 (the fp16 scheme uses 1/256, mlx_trunk.py:14-19, :47-48).
+ * ld % 8 == 0, ld >= L; ldx % 8 == 0, ldx >= L. Pointers 16-byte aligned.
+ */
+int tmu_contract(const esm_half* a, const esm_half* b, esm_half* x, int batch, int L, int ld, int ldx, float scale,
+                 void* stream);
+
+/*
+ * Kernel (c): norm_mix LayerNorm over c of the channel-major contraction ->
+ * proj_emit -> * sigmoid(proj_gate(LN_in(z))) [-> * mask] [-> + z], written
+ * cell-major.
+ *
+ * Replaces, in the reference:
+ *   ln_cf_to_cl(contracted, ln_mix_w, ln_mix_b, mix_eps)   mlx_trunk_kernels.py:152-160 (MSL :107-147)
+ *   mixed @ w_emit; n @ w_out_gate                         mlx_trunk_kernels.py:224-225
+ *   resgate_ln's z + m*sigmoid(g)  (residual = 1)          mlx_trunk_kernels.py:165-190
+ *   fast_trunk._trimul_forward lines 31-32                 fast_trunk.py:31-32
+ *
+ * x        [B, c, L, ldx] fp16 contraction output (as written by tmu_contract).
+ * z        [B, L, L, C] fp16 pair tensor (the gate is recomputed from LN_in(z)).
+ * mask     [B, L, L] fp16 or NULL; used only when out_mask != 0 (the reference
+ *          does not mask the update: off by default).
+ * ln_in_*  norm_start (C); ln_mix_* norm_mix (c); eps values as given.
+ * w_emit   [C, c] fp16 proj_emit.weight; w_gate [C, C] fp16 proj_gate.weight.
+ * out      [B, L, L, C] fp16: the update, or z + update when residual != 0
+ *          (out may alias z only when residual != 0).
+ * Supported: C = c = 128.
+ */
+int tmu_epilogue(const esm_half* x, int ldx, const esm_half* z, const esm_half* mask, const float* ln_in_w,
+                 const float* ln_in_b, float ln_in_eps, const float* ln_mix_w, const float* ln_mix_b,
+                 float ln_mix_eps, const esm_half* w_emit, const esm_half* w_gate, esm_half* out, int B, int L,
+                 int C, int c, int residual, int out_mask, void* stream);
+
+/*
+ * One whole triangle multiplicative update: kernels (a), (b), (c) in sequence on
+ * `stream`, with the fp16 range scheme of the reference's fp16 trunk (the
+ * contraction is stored as x/256 and norm_mix's eps divided by 256^2, an exact
+ * identity: mlx_trunk.py:14-19, :47-48, :114).
+ *
+ * Replaces fast_trunk._trimul_forward (fast_trunk.py:19-32), i.e. the per-module
+ * forward(pair_grid, visibility) -> update the reference's variant mechanism
+ * binds (fast_trunk.py:57), and mlx_trunk_kernels._trimul (mlx_trunk_kernels.py:210-229).
+ *
+ * workspace: tmu_workspace_bytes(B, L, c) bytes, 256-byte aligned, caller-owned.
+ * outgoing: 1 = "outgoing edges" update, 0 = "incoming edges".
+ */
+int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, const float* ln_in_b, float ln_in_eps,
+                const esm_half* w_bundle, const float* ln_mix_w, const float* ln_mix_b, float ln_mix_eps,
+                const esm_half* w_emit, const esm_half* w_gate, esm_half* out, void* workspace, int B, int L, int C,
+                int c, int outgoing, int residual, int out_mask, void* stream);
+
+/*
+ * Kernel (d): MLX-affine 8-bit weight-only linear, y = x . W^T with
+ * W[n, k] = RN_fp16(s[n, k/64] * q[n, k] + b[n, k/64]) (dequantised in registers,
+ * one fp16 FMA rounding) and fp32 accumulation; y rounded once to fp16.
+ *
+ * Replaces mx.quantized_matmul(x, w, s, b, transpose=True, group_size=64, bits=8)
+ * (mlx_esmc.py:78-81; weights from mlx_esmc.py:53-75). The reference packs codes
+ * four per uint32, little-endian: byte-identical to the row-major uint8 [N, K]
+ * taken here.
+ *
+ * x [M, K] fp16; q [N, K] uint8; s, b [N, K/group] fp16; y [M, N] fp16.
+ * Supported: group = 64, K % 64 == 0, N % 64 == 0, M >= 1.
+ */
+int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* y, int M, int K,
+              int N, int group, void* stream);
+
+/*
+ * Dequantise only: w[n, k] = RN_fp16(s[n, k/group] * q[n, k] + b[n, k/group]),
+ * the exact weights q8_linear multiplies by (for the bit-exact check).
+ * q [N, K] uint8; s, b [N, K/group] fp16; w [N, K] fp16. group = 64, K % 64 == 0.
+ */
+int q8_dequant(const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* w, int N, int K, int group,
+               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ESMFOLD2_AMD_H */

@@ -1,0 +1,89 @@
+"""CPU tests of the C ABI: the library loads, exports every declared symbol, and
+rejects bad arguments before launching anything (no GPU needed for these paths)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "esmfold2_amd.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*([a-z_0-9]+)\s*\(", src, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg.capi.lib(require_gpu=False)
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for n in ("tmu_project", "tmu_contract", "tmu_epilogue", "tmu_forward", "q8_linear", "q8_dequant",
+              "esm_last_error", "esm_version", "tmu_workspace_bytes", "tmu_leading_dim"):
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported_and_bound(pkg, lib):
+    handle = ctypes.CDLL(pkg.capi.lib_path())
+    for name in declared_functions():
+        assert hasattr(handle, name), f"{name} declared in the header but not exported"
+        assert name in pkg.capi.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(pkg.capi.SIGNATURES) == set(declared_functions())
+
+
+def test_version_and_sizes(lib):
+    assert b"gfx950" in lib.esm_version()
+    assert lib.tmu_leading_dim(238) == 240 and lib.tmu_leading_dim(240) == 240 and lib.tmu_leading_dim(1) == 8
+    # 3 planes of B*c*L*ld fp16, each rounded to 256 bytes
+    plane = 1 * 128 * 238 * 240 * 2
+    assert lib.tmu_workspace_bytes(1, 238, 128) == 3 * ((plane + 255) // 256 * 256)
+    assert lib.tmu_workspace_bytes(0, 238, 128) == 0
+
+
+def _err(lib):
+    return lib.esm_last_error().decode()
+
+
+def test_rejects_unsupported_channels(lib):
+    rc = lib.tmu_project(None, None, None, None, 1e-5, None, None, None, 1, 8, 256, 256, 8, 0, None)
+    assert rc == -4 and "supported" in _err(lib)
+    rc = lib.tmu_forward(*([None] * 4), 1e-5, None, None, None, 1e-5, None, None, None, None, 1, 8, 64, 64, 1, 0, 0,
+                         None)
+    assert rc == -4
+
+
+def test_rejects_null_and_bad_shapes(lib):
+    assert lib.tmu_project(None, None, None, None, 1e-5, None, None, None, 1, 8, 128, 128, 8, 0, None) == -1
+    assert lib.tmu_contract(None, None, None, 4, 8, 8, 8, 1.0, None) == -1
+    assert lib.tmu_contract(None, None, None, -1, 8, 8, 8, 1.0, None) == -2
+    assert lib.q8_linear(None, None, None, None, None, 4, 100, 64, 64, None) == -2  # K % 64
+    assert lib.q8_linear(None, None, None, None, None, 4, 128, 64, 32, None) == -4  # group 32
+    assert lib.q8_dequant(None, None, None, None, 64, 64, 64, None) == -1
+    # misaligned leading dimension (not a multiple of 8): checked before any pointer is used
+    fake = ctypes.c_void_p(4096)
+    assert lib.tmu_contract(fake, fake, fake, 1, 10, 12, 16, 1.0, None) == -2
+    assert "multiples of 8" in _err(lib)
+    # misaligned pointers
+    odd = ctypes.c_void_p(4096 + 2)
+    assert lib.tmu_contract(odd, fake, fake, 1, 10, 16, 16, 1.0, None) == -3
+
+
+def test_empty_inputs_are_a_no_op(lib):
+    assert lib.tmu_project(None, None, None, None, 1e-5, None, None, None, 0, 0, 128, 128, 0, 0, None) == 0
+    assert lib.tmu_contract(None, None, None, 0, 0, 0, 0, 1.0, None) == 0
+    assert lib.q8_linear(None, None, None, None, None, 0, 64, 64, 64, None) == 0
+    assert _err(lib) == ""
+
+
+def test_python_wrappers_refuse_cpu_tensors(pkg):
+    import torch
+    from oracle import tmu
+    p = tmu.draw_weights(torch.Generator().manual_seed(0), 128, 128, True)
+    with pytest.raises(Exception):
+        pkg.trimul.TriMul.from_weights(p, device="cpu")(torch.zeros(1, 4, 4, 128))
