@@ -54,7 +54,20 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-q8", action="store_true", help="skip the q8 linear figures")
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 64 MiB device copy 10 times (counter calibration under rocprofv3)")
     return ap.parse_args()
+
+
+def copy_probe(dev, reps: int = 10, nbytes: int = 64 << 20):
+    """A plain device-to-device copy of a known size: under rocprofv3 --pmc its FETCH_SIZE /
+    WRITE_SIZE per dispatch calibrate those counters (expected: nbytes each)."""
+    import torch
+    src = torch.ones(nbytes // 2, dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def cpu_baseline(z, po, pi):
@@ -231,6 +244,8 @@ def main():
                                       "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK}
         out["q8"] = qres
 
+    if args.copy_probe:
+        copy_probe(dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(z, po, pi)
         out["speedup_vs_cpu"] = out["value"] / out["cpu_baseline"]["value"]

@@ -111,7 +111,7 @@ int tmu_contract(const esm_half* a, const esm_half* b, esm_half* x, int batch, i
     return fail(ESM_ERR_SHAPE, "tmu_contract: ld=%d ldx=%d must be multiples of 8 and >= L=%d", ld, ldx, L);
   if (!aligned16(a) || !aligned16(b) || !aligned16(x))
     return fail(ESM_ERR_ALIGN, "tmu_contract: a, b, x must be 16-byte aligned");
-  esm::ContractArgs args{H(a), H(b), H(x), batch, L, ld, ldx, scale, (L + esm::kContractTile - 1) / esm::kContractTile};
+  esm::ContractArgs args{H(a), H(b), H(x), batch, L, ld, ldx, scale};
   return hip_status(esm::launch_contract(args, (hipStream_t)stream), "tmu_contract launch");
 }
 
@@ -138,8 +138,7 @@ int tmu_epilogue(const esm_half* x, int ldx, const esm_half* z, const esm_half* 
   const long long ntiles = (long long)B * L * e.tiles_per_line;
   if (ntiles > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_epilogue: too many tiles");
   e.ntiles = (int)ntiles;
-  const int per_cu = 2;
-  const long long cap = (long long)cu_count() * per_cu;
+  const long long cap = cu_count();  // one persistent workgroup per CU (1 wave per SIMD)
   const int grid = (int)(ntiles < cap ? ntiles : cap);
   return hip_status(esm::launch_epilogue(e, grid, (hipStream_t)stream), "tmu_epilogue launch");
 }

@@ -38,6 +38,34 @@ DEV f32x4 mfma16(half8 a, half8 b, f32x4 c) {
 DEV int acc_row32(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
 DEV half8 ld16(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
+
+// --- buffer (descriptor-based) global access -----------------------------------------
+// A raw buffer resource with a wave-uniform base and a 2 GB range. A lane whose byte
+// offset is kOOB (>= the range) is out of bounds: its load returns zeros and its store is
+// dropped by the hardware. Guarding with kOOB instead of a branch keeps every memory
+// instruction unconditional, so the compiler can count outstanding loads exactly and a
+// prefetch issued one tile ahead really stays in flight.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kBufRange = 0x7ffffff0;
+// Word 3 of a gfx9-family (CDNA) raw buffer descriptor: 32-bit data format, no swizzle.
+constexpr int kBufWord3 = 0x00020000;
+
+DEV rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, kBufRange, kBufWord3);
+}
+DEV half8 bload16(rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return __builtin_bit_cast(half8, v);
+}
+DEV void bstore16(rsrc_t r, uint32_t off, half8 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)off, 0, 0);
+}
+DEV void bstore8(rsrc_t r, uint32_t off, half4 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (int)off, 0, 0);
+}
+DEV uint16_t bload2(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0); }
+DEV float h2f(uint16_t bits) { return (float)__builtin_bit_cast(half_t, bits); }
 DEV void st16(half_t* p, half8 v) { *reinterpret_cast<half8*>(p) = v; }
 
 DEV half8 zero_half8() {
@@ -48,11 +76,17 @@ DEV half8 zero_half8() {
 }
 
 // Sum over the 16 lanes of a DPP row (lanes 16k .. 16k+15); every lane gets the sum.
+// DPP row rotations (row_ror:8, 4, 2, 1) stay in the VALU: no LDS round trip per step.
+// After rotating by 8, 4, 2 and 1 and adding, each lane has added all 16 lanes once.
+template <int CTRL>
+DEV float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
 DEV float row16_sum(float v) {
-  v += __shfl_xor(v, 8, 16);
-  v += __shfl_xor(v, 4, 16);
-  v += __shfl_xor(v, 2, 16);
-  v += __shfl_xor(v, 1, 16);
+  v += dpp_f32<0x128>(v);  // row_ror:8
+  v += dpp_f32<0x124>(v);  // row_ror:4
+  v += dpp_f32<0x122>(v);  // row_ror:2
+  v += dpp_f32<0x121>(v);  // row_ror:1
   return v;
 }
 

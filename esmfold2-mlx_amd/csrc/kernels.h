@@ -29,7 +29,6 @@ struct ContractArgs {
   half_t* x;            // [batch, L, ldx]
   int batch, L, ld, ldx;
   float scale;
-  int tiles;            // tiles per side: ceil(L / 128)
 };
 
 struct EpilogueArgs {
@@ -62,8 +61,6 @@ struct Q8Args {
 
 // Cells per tile of the per-cell kernels (a) and (c).
 constexpr int kCellTile = 64;
-// Output tile side of the contraction.
-constexpr int kContractTile = 128;
 
 // Each launcher returns the hipError_t of the launch.
 hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s);

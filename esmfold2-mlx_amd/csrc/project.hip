@@ -1,19 +1,29 @@
 // Kernel (a): input LayerNorm -> C->4c projection (MFMA) -> sigmoid gates ->
 // pair mask -> channel-major operands a, b.
 //
-// Persistent: each workgroup keeps its share of proj_bundle.weight in VGPRs for
-// the whole launch and walks cell tiles with a grid stride. A tile is 64 cells
-// along one "line" of the pair grid: cells (line, pos0..pos0+63) for the
-// outgoing layout, cells (pos0..pos0+63, line) for the transposed (incoming)
-// layout. Either way each cell's C channels are one contiguous 256-byte read and
-// each output row segment (one channel, 64 positions) is one contiguous 128-byte
-// write, staged through LDS so every global access is a 16-byte vector.
+// Persistent, one 8-wave workgroup per CU (2 waves per SIMD), walking tiles of 64
+// cells along one "line" of the pair grid: cells (line, pos0..pos0+63) for the
+// outgoing layout, cells (pos0..pos0+63, line) for the transposed (incoming) layout.
+// Each cell's C channels are one contiguous 256-byte read.
 //
-// Wave w of the 4 computes channels [32w, 32w+32) of both a and b:
-//   acc[0] = s_a rows, acc[1] = g_a rows, acc[2] = s_b rows, acc[3] = g_b rows
-// so the signal and gate of one (channel, cell) land in the same lane and
-// register: the gate is applied in fp32 straight from the accumulators and
-// rounded once to fp16 (as the reference's gate_cf, mlx_trunk_kernels.py:60-64).
+// Waves 0-3 own channels [32w, 32w+32) of a, waves 4-7 the same channels of b; each
+// keeps its slice of proj_bundle.weight (signal and gate rows of those channels) in
+// VGPRs as MFMA B-fragments for the whole launch. The projection runs as
+//   D[cell][channel] = LN(z)[cell][:] . W[channel][:]   (v_mfma_f32_32x32x16_f16)
+// with the two 32-cell halves of a tile interleaved, so 4 independent accumulator
+// chains keep the MFMA pipe full (the 16x16x32 form needs ~16 chains for the same
+// rate). Each lane ends with groups of 4 consecutive cells of one channel for the
+// signal and the gate alike:
+// the gate is applied in fp32 straight from the accumulators and rounded once to
+// fp16 (as the reference's gate_cf, mlx_trunk_kernels.py:60-64). The results are
+// staged per wave in LDS and leave as whole 128-byte row segments (8 lanes x 16 B
+// per channel row): scattered 32-byte pieces of rows measured 2x slower.
+//
+// Per tile: LayerNorm (16 lanes per cell) into a double-buffered LDS tile, one
+// barrier, then MFMA + gate + staging + store. The next tile's z is loaded while
+// this one computes. Every global access is an unconditional buffer
+// instruction (out-of-range lanes use an offset the hardware drops), so the
+// compiler's wait counts stay exact and the prefetch stays in flight.
 #include "common.h"
 #include "kernels.h"
 
@@ -24,28 +34,47 @@ constexpr int C = 128;                 // pair channels
 constexpr int CL = 128;                // latent channels
 constexpr int TM = kCellTile;          // cells per tile
 constexpr int NS = C + 8;              // LDS row stride (halfs) of the normalised tile
-constexpr int SS = TM + 8;             // LDS row stride (halfs) of the output staging rows
+constexpr int NW = 8;                  // waves per workgroup
+constexpr int CPW = 2 * CL / NW;       // channels per wave (of a for waves 0-3, of b for 4-7)
+constexpr int CPT = TM * 16 / (NW * 64);  // cells LayerNormed per thread per tile
+static_assert(CPW == 32, "one 32-column MFMA tile of channels per wave");
+static_assert(TM == 64, "a staged output row is 64 cells = 128 bytes = 8 chunks");
 }  // namespace
 
-__global__ __launch_bounds__(256, 1) void tmu_project_kernel(ProjectArgs p) {
-  __shared__ __align__(16) half_t n_s[TM * NS];
-  __shared__ __align__(16) half_t st_s[4][2][32 * SS];
-  __shared__ float m_s[TM];
+// Output staging: per wave, 32 channel rows of 64 cells (128 bytes, 8 chunks of 16 B),
+// chunk q of row ch stored at physical chunk q ^ ((ch >> 1) & 7). The 8-byte writes of
+// one accumulator group (32 rows, 2 lanes each) take the minimum two passes and the
+// 16-byte reads of two whole rows cover all 64 banks once.
+DEV int st_off(int ch, int cell) {  // in halfs
+  return ch * TM + 8 * ((cell >> 3) ^ ((ch >> 1) & 7)) + (cell & 7);
+}
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+template <bool HAS_MASK>
+__global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) {
+  __shared__ __align__(16) half_t n_s[2][TM * NS];
+  __shared__ __align__(16) float m_s[2][TM];
+  __shared__ __align__(16) half_t st_s[NW][CPW * TM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps descriptors scalar
   const int L = p.L;
+  constexpr bool has_mask = HAS_MASK;
 
-  // This wave's weight rows as MFMA A-fragments: rt = 0 s_a, 1 g_a, 2 s_b, 3 g_b.
-  half8 wr[4][C / 16];
-  {
-    const int base[4] = {0, 2 * CL, CL, 3 * CL};
-    const int row = 32 * wave + (lane & 31);
+  // Weight B-fragments: column = channel, k = 16 ks + 8 (lane/32) + e. Rows of
+  // proj_bundle.weight: signal s_a = [0, c), s_b = [c, 2c); gate g_a = [2c, 3c), g_b = [3c, 4c).
+  const int is_b = wave >= NW / 2;
+  const int ch_base = CPW * (wave - is_b * (NW / 2));  // first channel of this wave (of a or b)
+  half8 ws[C / 16], wg[C / 16];
+  auto load_weights = [&] {
+    const int ch = ch_base + (lane & 31);
+    const half_t* srow = p.w + (size_t)(is_b * CL + ch) * C;
+    const half_t* grow = p.w + (size_t)((2 + is_b) * CL + ch) * C;
 #pragma unroll
-    for (int rt = 0; rt < 4; rt++)
-#pragma unroll
-      for (int ks = 0; ks < C / 16; ks++)
-        wr[rt][ks] = ld16(p.w + (size_t)(base[rt] + row) * C + ks * 16 + 8 * (lane >> 5));
-  }
+    for (int ks = 0; ks < C / 16; ks++) {
+      ws[ks] = ld16(srow + 16 * ks + 8 * (lane >> 5));
+      wg[ks] = ld16(grow + 16 * ks + 8 * (lane >> 5));
+    }
+  };
   // LayerNorm parameters of this lane's 8 channels.
   const int ch0 = (lane & 15) * 8;
   float g[8], bb[8];
@@ -55,79 +84,134 @@ __global__ __launch_bounds__(256, 1) void tmu_project_kernel(ProjectArgs p) {
     bb[e] = p.ln_b[ch0 + e];
   }
 
-  for (int tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
+  // Tile coordinates: `line` is the fixed grid index, positions pos0 .. pos0+63 vary.
+  auto coords = [&](int tile, int& bi, int& line, int& pos0) {
     const int bl = tile / p.tiles_per_line;
-    const int pos0 = (tile - bl * p.tiles_per_line) * TM;
-    const int bi = bl / L, line = bl - bi * L;
-    const size_t plane = (size_t)bi * L * L;
+    pos0 = (tile - bl * p.tiles_per_line) * TM;
+    bi = bl / L;
+    line = bl - bi * L;
+  };
+  const uint32_t cstride = p.transpose ? (uint32_t)L : 1u;  // cell stride along the tile
 
-    // 1. Load 64 cells (16 lanes per cell, 8 channels per lane), LayerNorm, -> LDS.
+  // Issue one tile's loads: z (16 lanes per cell, 8 channels per lane) and the raw mask.
+  // A tile index past the end (the pipeline's last prefetch) loads nothing.
+  auto load_tile = [&](int tile, half8 (&zq)[CPT], uint16_t (&mq)[CPT]) {
+    const bool live = tile < p.ntiles;
+    int bi, line, pos0;
+    coords(live ? tile : 0, bi, line, pos0);
+    const size_t cb = (size_t)bi * L * L + (p.transpose ? (size_t)pos0 * L + line : (size_t)line * L + pos0);
+    const rsrc_t rz = make_rsrc(p.z + cb * C);
+    const rsrc_t rm = make_rsrc(has_mask ? (const void*)(p.mask + cb) : (const void*)p.z);
+    (void)rm;
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-      const int cl = (tid >> 4) + 16 * it;
-      const int pos = pos0 + cl;
-      half8 h = zero_half8();
-      float mval = 0.f;  // cells past L get a zero mask so their padded outputs are exactly 0
-      if (pos < L) {
-        const size_t cell = plane + (p.transpose ? (size_t)pos * L + line : (size_t)line * L + pos);
-        h = ld16(p.z + cell * C + ch0);
-        mval = p.mask ? (float)p.mask[cell] : 1.f;
-      }
+    for (int it = 0; it < CPT; it++) {
+      const int cl = (tid >> 4) + (NW * 4) * it;
+      const bool ok = live && pos0 + cl < L;
+      zq[it] = bload16(rz, ok ? (uint32_t)(cl * cstride * C + ch0) * 2u : kOOB);
+      if (has_mask) mq[it] = bload2(rm, ok ? (uint32_t)(cl * cstride) * 2u : kOOB);
+    }
+  };
+
+  auto process_tile = [&](int tile, const half8 (&zq)[CPT], const uint16_t (&mq)[CPT], int nb) {
+    int bi, line, pos0;
+    coords(tile, bi, line, pos0);
+    half_t* ns = n_s[nb];
+    // 1. LayerNorm -> LDS. Double-buffered: a wave still in the previous tile's MFMA phase
+    //    reads the other buffer; this one was last read two tiles ago, before the barrier
+    //    of the previous tile.
+#pragma unroll
+    for (int it = 0; it < CPT; it++) {
+      const int cl = (tid >> 4) + (NW * 4) * it;
       float v[8];
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = (float)h[e];
+      for (int e = 0; e < 8; e++) v[e] = (float)zq[it][e];
       ln_row128(v, g, bb, p.eps);
       half8 o;
 #pragma unroll
       for (int e = 0; e < 8; e++) o[e] = (half_t)v[e];
-      st16(&n_s[cl * NS + ch0], o);
-      if ((lane & 15) == 0) m_s[cl] = mval;
+      st16(&ns[cl * NS + ch0], o);
+      // cells past L get a zero mask so their padded outputs [L, ld) are exactly 0
+      const float mval = pos0 + cl < L ? (has_mask ? h2f(mq[it]) : 1.f) : 0.f;
+      if ((lane & 15) == 0) m_s[nb][cl] = mval;
     }
     __syncthreads();
 
-    // 2. Projection on MFMA, gate in fp32, stage fp16 channel rows in LDS.
+    // 2. Projection of both 32-cell halves (4 accumulator chains), gate in fp32, groups of
+    //    4 cells of one channel per lane staged (8 bytes) in this wave's LDS rows.
+    half_t* st = st_s[wave];
+    f32x16 as[2], ag[2];
 #pragma unroll
-    for (int cs = 0; cs < TM / 32; cs++) {
-      f32x16 acc[4];
-#pragma unroll
-      for (int rt = 0; rt < 4; rt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[rt][r] = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < C / 16; ks++) {
-        const half8 bf = ld16(&n_s[(cs * 32 + (lane & 31)) * NS + ks * 16 + 8 * (lane >> 5)]);
-#pragma unroll
-        for (int rt = 0; rt < 4; rt++) acc[rt] = mfma32(wr[rt][ks], bf, acc[rt]);
-      }
-      const int cl = cs * 32 + (lane & 31);
-      const float mval = m_s[cl];
+    for (int h = 0; h < 2; h++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int ch = acc_row32(r, lane);
-        st_s[wave][0][ch * SS + cl] = (half_t)(acc[0][r] * sigmoidf_fast(acc[1][r]) * mval);
-        st_s[wave][1][ch * SS + cl] = (half_t)(acc[2][r] * sigmoidf_fast(acc[3][r]) * mval);
+        as[h][r] = 0.f;
+        ag[h][r] = 0.f;
       }
-    }
-    __syncthreads();
-
-    // 3. Store this wave's 32 channel rows of a and b: 8 lanes x 16 B per row.
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const int which = u >> 2;
-      const int ch = (u & 3) * 8 + (lane >> 3);
-      const int q = lane & 7;
-      const int pos = pos0 + q * 8;
-      if (pos < p.ld) {
-        const half8 v = ld16(&st_s[wave][which][ch * SS + q * 8]);
-        half_t* dst = (which ? p.b : p.a) + (((size_t)bi * CL + 32 * wave + ch) * L + line) * p.ld + pos;
-        st16(dst, v);
+    for (int ks = 0; ks < C / 16; ks++) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const half8 af = ld16(&ns[(32 * h + (lane & 31)) * NS + 16 * ks + 8 * (lane >> 5)]);
+        as[h] = mfma32(af, ws[ks], as[h]);
+        ag[h] = mfma32(af, wg[ks], ag[h]);
       }
     }
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++) {
+        const int c4 = 32 * h + acc_row32(4 * r4, lane);  // first of this group's 4 cells
+        const f32x4 m4 = *reinterpret_cast<const f32x4*>(&m_s[nb][c4]);
+        half4 v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = (half_t)(as[h][4 * r4 + e] * sigmoidf_fast(ag[h][4 * r4 + e]) * m4[e]);
+        *reinterpret_cast<half4*>(&st[st_off(lane & 31, c4)]) = v;
+      }
+    // The staging rows are private to the wave and a wave's LDS operations complete in
+    // order; this only keeps the compiler from moving the reads above the writes.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // 3. Whole 128-byte row segments: 8 lanes x 16 B per channel row, 8 rows per store.
+    //    Chunks at or past ld are dropped by the buffer range check.
+    const size_t row0 = ((size_t)bi * CL + ch_base) * L + line;  // this wave's first channel row
+    const rsrc_t ro = make_rsrc((is_b ? p.b : p.a) + row0 * p.ld + pos0);
+    const int q = lane & 7;
+    const bool okq = pos0 + q * 8 < p.ld;
+#pragma unroll
+    for (int u = 0; u < CPW / 8; u++) {
+      const int ch = 8 * u + (lane >> 3);
+      const uint32_t off = okq ? (uint32_t)((size_t)ch * L * p.ld + q * 8) * 2u : kOOB;
+      bstore16(ro, off, ld16(&st[st_off(ch, q * 8)]));
+    }
+  };
+
+  // Software pipeline: the next tile's loads are in flight while this tile computes
+  // (ping-pong register buffers, unrolled by two so no register copy waits on a load; every
+  // step issues the same memory instructions, so the waits count exactly). Start-up order:
+  // the first tile's z goes out before the 16 KB of weights per wave, so its LayerNorm
+  // overlaps the weight stream.
+  const int G = gridDim.x;
+  half8 zA[CPT], zB[CPT];
+  uint16_t mA[CPT] = {}, mB[CPT] = {};
+  int tile = blockIdx.x;
+  load_tile(tile, zA, mA);
+  load_weights();
+  for (; tile < p.ntiles; tile += 2 * G) {
+    load_tile(tile + G, zB, mB);
+    process_tile(tile, zA, mA, 0);
+    if (tile + G >= p.ntiles) break;
+    load_tile(tile + 2 * G, zA, mA);
+    process_tile(tile + G, zB, mB, 1);
   }
 }
 
 hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL(tmu_project_kernel, dim3(grid), dim3(256), 0, s, a);
+  if (a.mask)
+    hipLaunchKernelGGL(tmu_project_kernel<true>, dim3(grid), dim3(NW * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL(tmu_project_kernel<false>, dim3(grid), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
