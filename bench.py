@@ -46,6 +46,23 @@ def alg_counts(L: int, C: int, c: int):
     }
 
 
+PROFILE_COUNTERS = os.path.join(ROOT, "profiles", "tmu_pair_L238_counters.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch per kernel from the committed rocprofv3 counter summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by a plain-copy calibration); {} if absent."""
+    out = {}
+    try:
+        for line in open(PROFILE_COUNTERS):
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes":
+                out[parts[1]] = int(parts[2])
+    except OSError:
+        pass
+    return out
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -193,14 +210,17 @@ def main():
                    "gbs": counts[k]["bytes"] / t / 1e9,
                    "mfma_frac": counts[k]["flops"] / t / MFMA_F16_PEAK,
                    "hbm_frac": counts[k]["bytes"] / t / HBM_PEAK}
+    traffic = measured_traffic()
+    for k in kinds:
+        kern[k]["traffic_bytes"] = traffic.get(f"tmu_{k}_kernel")
     dom = max(kinds, key=lambda k: kern[k]["us"])
     if dom == "contract":
         roof = {"bound": "mfma", "achieved": kern[dom]["tflops"], "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
-                "frac": kern[dom]["mfma_frac"], "traffic": None, "kernel": "tmu_contract_kernel",
+                "frac": kern[dom]["mfma_frac"], "traffic": kern[dom]["traffic_bytes"], "kernel": "tmu_contract_kernel",
                 "per_launch": f"{counts[dom]['flops'] / 1e9:.3f} GFLOP"}
     else:
         roof = {"bound": "hbm", "achieved": kern[dom]["gbs"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": kern[dom]["hbm_frac"], "traffic": None, "kernel": f"tmu_{dom}_kernel",
+                "frac": kern[dom]["hbm_frac"], "traffic": kern[dom]["traffic_bytes"], "kernel": f"tmu_{dom}_kernel",
                 "per_launch": f"{counts[dom]['bytes'] / 1e6:.2f} MB"}
 
     pair_flops = 2 * sum(v["flops"] for v in counts.values())
