@@ -90,6 +90,33 @@ DEV float row16_sum(float v) {
   return v;
 }
 
+// --- weight staging ----------------------------------------------------------------------
+// Weight rows of 128 halfs (256 B) go through LDS so that the global reads are fully
+// coalesced (each load instruction of a workgroup covers NT*16 contiguous bytes). Read
+// straight into MFMA fragments, every instruction would touch 32 different rows, and the
+// per-CU L1 path would need several times as many cycles for the same bytes. In LDS the
+// 16-byte chunk j of row r sits at chunk j ^ (r & 15): the fragment reads of 16
+// consecutive rows at one logical chunk hit 16 distinct chunk positions (all 64 banks).
+template <int ROWS, int NT>
+struct RowStage {
+  static constexpr int kPer = ROWS * 16 / NT;  // 16-byte chunks per thread
+  static_assert(ROWS * 16 % NT == 0, "whole chunks per thread");
+  half8 v[kPer];
+  DEV void load(const half_t* src, int tid) {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) v[i] = ld16(src + 8 * (tid + NT * i));
+  }
+  DEV void store(half_t* dst, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int q = tid + NT * i, r = q >> 4, j = q & 15;
+      st16(dst + r * 128 + 8 * (j ^ (r & 15)), v[i]);
+    }
+  }
+};
+// Logical 16-byte chunk j (halfs 8j .. 8j+7) of staged row r.
+DEV half8 staged_chunk(const half_t* s, int r, int j) { return ld16(s + r * 128 + 8 * (j ^ (r & 15))); }
+
 DEV float sigmoidf_fast(float x) {
   // 1 / (1 + e^-x): v_exp_f32 and v_rcp_f32 (about 1 ulp each); saturates
   // cleanly to 0 and 1 at +-inf.

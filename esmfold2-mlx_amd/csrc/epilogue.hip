@@ -68,13 +68,26 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_epilogue_kernel(EpilogueArgs p
 
   // Weight A-fragments: row = output channel o = 32 og + lane%32, k = 16 ks + 8 (lane/32) + e.
   const int og = wave & 3, chalf = wave >> 2;
+  // proj_emit, then proj_gate, stream through LDS (the fp32 staging tile, 32 KB, is free
+  // until the first tile's GEMMs, two barriers into the loop) in coalesced rounds; both
+  // rounds' loads are in flight together.
   half8 we[CL / 16], wg[C / 16];
   auto load_weights = [&] {
+    static_assert(C * CL * 2 <= TM * OS * 4 && C * C * 2 <= TM * OS * 4, "a weight fits the staging tile");
+    half_t* w_s = reinterpret_cast<half_t*>(o_s);
+    RowStage<C, NW * 64> r0, r1;
+    r0.load(p.w_emit, tid);
+    r1.load(p.w_gate, tid);
     const int o = OPW * og + (lane & 31);
+    r0.store(w_s, tid);
+    __syncthreads();
 #pragma unroll
-    for (int ks = 0; ks < CL / 16; ks++) we[ks] = ld16(p.w_emit + (size_t)o * CL + 16 * ks + 8 * (lane >> 5));
+    for (int ks = 0; ks < CL / 16; ks++) we[ks] = staged_chunk(w_s, o, 2 * ks + (lane >> 5));
+    __syncthreads();
+    r1.store(w_s, tid);
+    __syncthreads();
 #pragma unroll
-    for (int ks = 0; ks < C / 16; ks++) wg[ks] = ld16(p.w_gate + (size_t)o * C + 16 * ks + 8 * (lane >> 5));
+    for (int ks = 0; ks < C / 16; ks++) wg[ks] = staged_chunk(w_s, o, 2 * ks + (lane >> 5));
   };
   const int ch0 = (lane & 15) * 8;
   float gin[8], bin[8], gmx[8], bmx[8];

@@ -8,7 +8,8 @@
 //
 // Waves 0-3 own channels [32w, 32w+32) of a, waves 4-7 the same channels of b; each
 // keeps its slice of proj_bundle.weight (signal and gate rows of those channels) in
-// VGPRs as MFMA B-fragments for the whole launch. The projection runs as
+// VGPRs as MFMA B-fragments for the whole launch, read once through LDS with coalesced
+// loads. The projection runs as
 //   D[cell][channel] = LN(z)[cell][:] . W[channel][:]   (v_mfma_f32_32x32x16_f16)
 // with the two 32-cell halves of a tile interleaved, so 4 independent accumulator
 // chains keep the MFMA pipe full (the 16x16x32 form needs ~16 chains for the same
@@ -54,6 +55,7 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
   __shared__ __align__(16) half_t n_s[2][TM * NS];
   __shared__ __align__(16) float m_s[2][TM];
   __shared__ __align__(16) half_t st_s[NW][CPW * TM];
+  __shared__ __align__(16) half_t w_s[2 * CL * C];  // weight staging, start-up only
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps descriptors scalar
@@ -64,16 +66,23 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
   // proj_bundle.weight: signal s_a = [0, c), s_b = [c, 2c); gate g_a = [2c, 3c), g_b = [3c, 4c).
   const int is_b = wave >= NW / 2;
   const int ch_base = CPW * (wave - is_b * (NW / 2));  // first channel of this wave (of a or b)
+  // The bundle streams through LDS in two coalesced rounds of 256 rows: the signal rows
+  // [0, 2c), then the gate rows [2c, 4c); both rounds' loads are in flight together.
   half8 ws[C / 16], wg[C / 16];
   auto load_weights = [&] {
-    const int ch = ch_base + (lane & 31);
-    const half_t* srow = p.w + (size_t)(is_b * CL + ch) * C;
-    const half_t* grow = p.w + (size_t)((2 + is_b) * CL + ch) * C;
+    RowStage<2 * CL, NW * 64> r0, r1;
+    r0.load(p.w, tid);
+    r1.load(p.w + 2 * CL * C, tid);
+    const int row = is_b * CL + ch_base + (lane & 31);
+    r0.store(w_s, tid);
+    __syncthreads();
 #pragma unroll
-    for (int ks = 0; ks < C / 16; ks++) {
-      ws[ks] = ld16(srow + 16 * ks + 8 * (lane >> 5));
-      wg[ks] = ld16(grow + 16 * ks + 8 * (lane >> 5));
-    }
+    for (int ks = 0; ks < C / 16; ks++) ws[ks] = staged_chunk(w_s, row, 2 * ks + (lane >> 5));
+    __syncthreads();
+    r1.store(w_s, tid);
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < C / 16; ks++) wg[ks] = staged_chunk(w_s, row, 2 * ks + (lane >> 5));
   };
   // LayerNorm parameters of this lane's 8 channels.
   const int ch0 = (lane & 15) * 8;
