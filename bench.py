@@ -13,7 +13,9 @@ Also reported on the same JSON line:
                 [238,10240]x[10240->2560] (time, TFLOP/s, GB/s);
   cpu_baseline  the CPU oracle (torch fp32 restatement of the reference's
                 _trimul_forward) on the host cores, a bounded sample of the same
-                workload (rank 0, N=1 only).
+                workload (rank 0, N=1 only). This leg is also the checker: the
+                benchmarked pair output and sampled q8 rows are compared with the
+                oracle's (the GPU leg itself imports nothing from oracle/).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--graph]
 """
@@ -87,23 +89,38 @@ def copy_probe(dev, reps: int = 10, nbytes: int = 64 << 20):
     torch.cuda.synchronize()
 
 
-def cpu_baseline(z, po, pi):
-    """The CPU oracle in fp32 on the host cores: 1 warm-up, median of 3 TMU pairs at L=238."""
+def cpu_baseline(z, po, pi, pair_out, q8_samples):
+    """The CPU oracle in fp32 on the host cores: 1 warm-up, median of 3 TMU pairs at L=238.
+    Also the checker of the GPU leg: the benchmarked pair output against the oracle's
+    (max|err| / RMS(update), bar 1e-2) and the sampled q8 rows (normwise, bar 1e-3)."""
+    import numpy as np
     import torch
-    from oracle import tmu
+    from oracle import q8 as oq8, tmu
     threads = torch.get_num_threads()
     zf = z.float()
+    fields = ("w_bundle", "w_emit", "w_gate", "ln_in_w", "ln_in_b", "ln_mix_w", "ln_mix_b", "ln_in_eps", "ln_mix_eps",
+              "outgoing")
+    po, pi = (tmu.TriMulWeights(**{f: getattr(p, f) for f in fields}) for p in (po, pi))
     with torch.no_grad():
-        tmu.trimul_pair(zf, None, po, pi)
+        ref = tmu.trimul_pair(zf, None, po, pi)
         ts = []
         for _ in range(3):
             t0 = time.perf_counter()
             tmu.trimul_pair(zf, None, po, pi)
             ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
+    upd_ref = ref.double() - z.double()
+    upd_got = pair_out.double() - z.double()
+    pair_err = float((upd_got - upd_ref).abs().max() / upd_ref.pow(2).mean().sqrt())
+    q8_err = {}
+    for name, (rows, x, q, s, b, y) in q8_samples.items():
+        yr = oq8.q8_linear(x[rows].numpy(), q.numpy(), s.numpy(), b.numpy())
+        q8_err[name] = float(np.linalg.norm(y - yr) / np.linalg.norm(yr))
+    ok = pair_err <= 1e-2 and all(e <= 1e-3 for e in q8_err.values())
     return {"value": L * L / t, "unit": "cells/s", "cores": threads, "kind": "port",
             "sample": f"TMU pair (out+in, residuals) at L={L}, C=c={C}, fp32 torch on CPU, median of 3 after 1 "
-                      f"warm-up, {t * 1e3:.1f} ms per pair"}
+                      f"warm-up, {t * 1e3:.1f} ms per pair",
+            "check": {"pair_max_err_over_rms": pair_err, "q8_rel_err_sample_rows": q8_err, "ok": ok}}
 
 
 def main():
@@ -114,12 +131,12 @@ def main():
     import torch
     from __graft_entry__ import load_package
     pkg = load_package()
-    from oracle import tmu, q8 as oq8
+    W = pkg.workloads
 
     lib = pkg.capi.lib()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    z, _, po, pi = tmu.make_pair_inputs(L, C, CL, seed=0, dtype=torch.float16)
+    z, _, po, pi = W.pair_inputs(L, C, CL, seed=0, dtype=torch.float16)
     t_out = pkg.trimul.TriMul.from_weights(po, device=dev)
     t_in = pkg.trimul.TriMul.from_weights(pi, device=dev)
     K = pkg.kernels
@@ -160,13 +177,12 @@ def main():
                 if events is not None:
                     events[(d, kind)][1].record(stream)
 
-    # correctness guard on the benchmarked configuration (cheap: one pair vs the fp32 oracle)
+    # the benchmarked configuration's output, checked against the oracle in the CPU leg
     step()
     torch.cuda.synchronize()
-    got = zbuf.double().cpu() - z.double()
-    with torch.no_grad():
-        ref = tmu.trimul_pair(z.float(), None, po, pi).double() - z.double()
-    rel_err = float((got - ref).abs().max() / ref.pow(2).mean().sqrt())
+    pair_out = zbuf.cpu()
+    if not torch.isfinite(pair_out.float()).all():
+        raise SystemExit("TMU pair output is not finite")
 
     for _ in range(args.warmup):
         step()
@@ -235,41 +251,47 @@ def main():
                    "launch": "hip graph" if graph is not None else "eager"},
         "pair_mfma_frac": pair_flops / (ms * 1e-3) / MFMA_F16_PEAK,
         "pair_hbm_frac": pair_bytes / (ms * 1e-3) / HBM_PEAK,
-        "max_err_over_rms": rel_err,
         "roofline": roof,
         "kernels": kern,
     }
 
+    q8_samples = {}
     if not args.no_q8:
         qres = {}
         for (Kd, Nd) in ((2560, 10240), (10240, 2560)):
-            xq, qq, sq, bq = oq8.make_q8_inputs(L, Kd, Nd, seed=Kd)
-            xt, qt = torch.from_numpy(xq).to(dev), torch.from_numpy(qq).to(dev)
-            st, bt = torch.from_numpy(sq).to(dev), torch.from_numpy(bq).to(dev)
+            xq, qq, sq, bq = W.q8_inputs(L, Kd, Nd, seed=Kd)
+            xt, qt, st, bt = (t.to(dev) for t in (xq, qq, sq, bq))
             y = torch.empty(L, Nd, dtype=torch.float16, device=dev)
+            ws = K.q8_workspace(L, Kd, Nd, device=dev)  # split-K partials when the tiles are too few
+            sbp = K.q8_pack_scales(st, bt)              # per-layer layout cache, built once
             for _ in range(5):
-                K.q8_linear(xt, qt, st, bt, out=y)
+                K.q8_linear(xt, qt, st, bt, out=y, workspace=ws, packed=sbp)
+            rows = [0, L // 2, L - 1]
+            name = f"{L}x{Kd}->{Nd}"
+            q8_samples[name] = (rows, xq, qq, sq, bq, y[rows].double().cpu().numpy())
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             e0.record(stream)
             reps = 50
             for _ in range(reps):
-                K.q8_linear(xt, qt, st, bt, out=y)
+                K.q8_linear(xt, qt, st, bt, out=y, workspace=ws, packed=sbp)
             e1.record(stream)
             torch.cuda.synchronize()
             t = e0.elapsed_time(e1) * 1e-3 / reps
             fl = 2 * L * Kd * Nd
             by = Nd * Kd + 2 * 2 * Nd * (Kd // 64) + 2 * L * Kd + 2 * L * Nd
-            qres[f"{L}x{Kd}->{Nd}"] = {"us": t * 1e6, "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
-                                      "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK}
+            qres[name] = {"us": t * 1e6, "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
+                          "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK, "split_k": ws is not None}
         out["q8"] = qres
 
     if args.copy_probe:
         copy_probe(dev)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(z, po, pi)
+        out["cpu_baseline"] = cpu_baseline(z, po, pi, pair_out, q8_samples)
         out["speedup_vs_cpu"] = out["value"] / out["cpu_baseline"]["value"]
     print(json.dumps(out), flush=True)
+    if not args.no_cpu and not out["cpu_baseline"]["check"]["ok"]:
+        raise SystemExit("the benchmarked outputs differ from the oracle beyond the bars")
 
 
 if __name__ == "__main__":

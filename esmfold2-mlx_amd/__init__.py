@@ -8,16 +8,16 @@ Modules:
   trimul           -- TriMul / TriMulPair: the forward(pair_grid, visibility) module contract
   q8               -- Q8Linear: the quantized_matmul(transpose=True, group 64, bits 8) contract
   var_hip_trimul   -- the reference-style variant plugin: apply(model)
-  smoke            -- one tiny GPU run checked against the CPU oracle
+  workloads        -- seeded synthetic inputs of the benchmark configurations
 """
 
 from . import build, capi  # noqa: F401
 
-__all__ = ["build", "capi", "kernels", "trimul", "q8", "var_hip_trimul", "smoke"]
+__all__ = ["build", "capi", "kernels", "trimul", "q8", "var_hip_trimul", "workloads"]
 
 
 def __getattr__(name):
-    if name in ("kernels", "trimul", "q8", "var_hip_trimul", "smoke"):
+    if name in ("kernels", "trimul", "q8", "var_hip_trimul", "workloads"):
         import importlib
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)

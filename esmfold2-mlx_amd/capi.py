@@ -28,6 +28,10 @@ SIGNATURES = {
     "tmu_forward": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _int, _int, _int,
                            _int, _int, _int, _int, _vp]),
     "q8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
+    "q8_linear_ws": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
+    "q8_linear_workspace_bytes": (_sz, [_int, _int, _int]),
+    "q8_packed_scales_bytes": (_sz, [_int, _int]),
+    "q8_pack_scales": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp]),
     "q8_dequant": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
 }
 

@@ -54,6 +54,30 @@ int cu_count() {
 
 constexpr int kMaxL = 4096;  // pair side limit: keeps every 32-bit tile index in range
 
+// q8 GEMM launch plan. A tile is kQ8TileM x kQ8TileN outputs; when the tiles alone
+// cannot fill the GPU, K is split over up to kQ8MaxSplits workgroups per tile (each
+// of the 4 waves keeps at least one 64-wide group) and the partials go through the
+// caller's workspace: [splits, M, N] fp32, summed by a second kernel.
+constexpr int kQ8MaxSplits = 16;
+constexpr int kQ8MaxK = 1 << 20;  // keeps every per-row byte offset far below 2^31
+struct Q8Plan {
+  int mtiles, ntiles, splits;
+  size_t bytes;
+};
+Q8Plan q8_plan(int M, int K, int N) {
+  Q8Plan p;
+  p.mtiles = (M + esm::kQ8TileM - 1) / esm::kQ8TileM;
+  p.ntiles = (N + esm::kQ8TileN - 1) / esm::kQ8TileN;
+  const long long tiles = (long long)p.mtiles * p.ntiles;
+  const int groups = K / 64;
+  long long sp = cu_count() / tiles;
+  if (sp > kQ8MaxSplits) sp = kQ8MaxSplits;
+  if (sp > groups / esm::kQ8Waves) sp = groups / esm::kQ8Waves;
+  p.splits = sp < 1 ? 1 : (int)sp;
+  p.bytes = (size_t)p.splits * M * N * sizeof(float);
+  return p;
+}
+
 using esm::half_t;
 inline const half_t* H(const esm_half* p) { return reinterpret_cast<const half_t*>(p); }
 inline half_t* H(esm_half* p) { return reinterpret_cast<half_t*>(p); }
@@ -171,20 +195,62 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
                       w_emit, w_gate, out, B, L, C, c, residual, out_mask, stream);
 }
 
-int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* y, int M, int K,
-              int N, int group, void* stream) {
+int q8_linear_ws(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, const uint32_t* sb,
+                 esm_half* y, int M, int K, int N, int group, void* workspace, size_t workspace_bytes, void* stream) {
   if (M < 0 || K < 0 || N < 0) return fail(ESM_ERR_SHAPE, "q8_linear: M=%d K=%d N=%d must be >= 0", M, K, N);
   if (group != 64) return fail(ESM_ERR_UNSUPPORTED, "q8_linear: group=%d (supported: 64)", group);
   if (M == 0 || N == 0) return ok();
   if (K == 0 || K % 64 != 0 || N % 64 != 0)
     return fail(ESM_ERR_SHAPE, "q8_linear: K=%d and N=%d must be positive multiples of 64", K, N);
+  if (K > kQ8MaxK) return fail(ESM_ERR_SHAPE, "q8_linear: K=%d too large (max %d)", K, kQ8MaxK);
+  if ((long long)N * K >= (1LL << 31) || (long long)M * K * 2 >= (1LL << 31))
+    return fail(ESM_ERR_SHAPE, "q8_linear: M=%d, K=%d, N=%d: x or q exceeds 2 GB", M, K, N);
   if (!x || !q || !s || !b || !y) return fail(ESM_ERR_NULL, "q8_linear: NULL pointer");
-  if (M > 65535 * 64) return fail(ESM_ERR_SHAPE, "q8_linear: M=%d too large", M);
   if (!aligned16(x) || !aligned16(q) || (reinterpret_cast<uintptr_t>(y) & 7u) != 0 ||
       (reinterpret_cast<uintptr_t>(s) & 1u) != 0 || (reinterpret_cast<uintptr_t>(b) & 1u) != 0)
     return fail(ESM_ERR_ALIGN, "q8_linear: x, q must be 16-byte aligned and y 8-byte aligned");
-  esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N};
+  Q8Plan pl = q8_plan(M, K, N);
+  if ((long long)pl.mtiles * pl.ntiles * pl.splits > 0x7fffffffLL)
+    return fail(ESM_ERR_SHAPE, "q8_linear: M=%d N=%d too large", M, N);
+  if (!workspace) {
+    pl.splits = 1;  // no workspace: one workgroup per tile, no partials
+  } else if (pl.splits > 1) {
+    if (workspace_bytes < pl.bytes)
+      return fail(ESM_ERR_SHAPE, "q8_linear: workspace of %zu bytes, %zu needed", workspace_bytes, pl.bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(ESM_ERR_ALIGN, "q8_linear: workspace must be 256-byte aligned");
+  }
+  if (sb && !aligned16(sb)) return fail(ESM_ERR_ALIGN, "q8_linear: packed scales must be 16-byte aligned");
+  esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits,
+                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear launch");
+}
+
+int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* y, int M, int K,
+              int N, int group, void* stream) {
+  return q8_linear_ws(x, q, s, b, nullptr, y, M, K, N, group, nullptr, 0, stream);
+}
+
+size_t q8_packed_scales_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 64 != 0) return 0;
+  return (size_t)((N + esm::kQ8TileN - 1) / esm::kQ8TileN) * (K / 64) * esm::kQ8TileN * sizeof(uint32_t);
+}
+
+int q8_pack_scales(const esm_half* s, const esm_half* b, uint32_t* sb, int N, int K, int group, void* stream) {
+  if (N < 0 || K < 0) return fail(ESM_ERR_SHAPE, "q8_pack_scales: N=%d K=%d must be >= 0", N, K);
+  if (group != 64) return fail(ESM_ERR_UNSUPPORTED, "q8_pack_scales: group=%d (supported: 64)", group);
+  if (N == 0 || K == 0) return ok();
+  if (K % 64 != 0) return fail(ESM_ERR_SHAPE, "q8_pack_scales: K=%d must be a multiple of 64", K);
+  if (!s || !b || !sb) return fail(ESM_ERR_NULL, "q8_pack_scales: NULL pointer");
+  if ((reinterpret_cast<uintptr_t>(s) & 1u) || (reinterpret_cast<uintptr_t>(b) & 1u) || !aligned16(sb))
+    return fail(ESM_ERR_ALIGN, "q8_pack_scales: s, b must be 2-byte and sb 16-byte aligned");
+  return hip_status(esm::launch_q8_pack(H(s), H(b), sb, N, K, (hipStream_t)stream), "q8_pack_scales launch");
+}
+
+size_t q8_linear_workspace_bytes(int M, int K, int N) {
+  if (M <= 0 || K <= 0 || N <= 0 || K % 64 != 0 || N % 64 != 0 || K > kQ8MaxK) return 0;
+  const Q8Plan pl = q8_plan(M, K, N);
+  return pl.splits > 1 ? pl.bytes : 0;
 }
 
 int q8_dequant(const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* w, int N, int K, int group,

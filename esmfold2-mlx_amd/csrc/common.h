@@ -54,6 +54,11 @@ constexpr int kBufWord3 = 0x00020000;
 DEV rsrc_t make_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, kBufRange, kBufWord3);
 }
+// A raw buffer resource whose range is exactly `bytes`: any offset at or past it
+// (including kOOB) loads zeros.
+DEV rsrc_t make_rsrc_n(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufWord3);
+}
 DEV half8 bload16(rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
   return __builtin_bit_cast(half8, v);
@@ -88,6 +93,17 @@ DEV float row16_sum(float v) {
   v += dpp_f32<0x122>(v);  // row_ror:2
   v += dpp_f32<0x121>(v);  // row_ror:1
   return v;
+}
+
+// --- workgroup order --------------------------------------------------------------------
+// The dispatcher deals workgroup ids round-robin to the 8 XCDs (each with its own L2).
+// This bijection of [0, n) gives each XCD a contiguous run of logical indices, so
+// logical neighbours that read the same operands share one L2.
+constexpr int kNumXcd = 8;
+DEV int xcd_remap(int id, int n) {
+  const int per = n / kNumXcd, rem = n % kNumXcd;
+  const int xcd = id % kNumXcd, slot = id / kNumXcd;
+  return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
 }
 
 // --- weight staging ----------------------------------------------------------------------

@@ -29,7 +29,6 @@ constexpr int KS = BK + 8;         // LDS row stride (halfs) of an operand stage
 constexpr int STAGE = (BM + BN) * KS;
 constexpr int CS = BN + 8;         // LDS row stride (halfs) of the output staging tile
 constexpr int SMEM = (2 * STAGE > BM * CS) ? 2 * STAGE : BM * CS;
-constexpr int NXCD = 8;
 constexpr int CHUNKS = (BM + BN) * BK / 8 / 256;  // 16-byte loads per thread per stage
 static_assert((BM + BN) * BK / 8 % 256 == 0, "stage must split evenly over 256 threads");
 static_assert(BM * 4 % 256 == 0, "A chunks must fill whole loader passes");
@@ -44,13 +43,7 @@ __global__ __launch_bounds__(256, 2) void tmu_contract_kernel(ContractArgs p) {
   const int L = p.L, ld = p.ld;
 
   // XCD-aware remap of the workgroup id to a logical block index (a bijection).
-  int t;
-  {
-    const int id = blockIdx.x, n = gridDim.x;
-    const int per = n / NXCD, rem = n % NXCD;
-    const int xcd = id % NXCD, slot = id / NXCD;
-    t = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
-  }
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int nrb = (L + BM - 1) / BM, ncb = (L + BN - 1) / BN;
   const int rb = t % nrb;
   const int cb = (t / nrb) % ncb;

@@ -57,7 +57,16 @@ struct Q8Args {
   const half_t* b;      // [N, K/64]
   half_t* y;            // [M, N]
   int M, K, N;
+  int mtiles, ntiles;   // tiles of kQ8TileM x kQ8TileN outputs
+  int splits;           // K ranges per tile (1: no workspace)
+  float* part;          // [splits, M, N] fp32 partials (splits > 1)
+  const uint32_t* sb;   // packed scales [ntiles, K/64, kQ8TileN] (b << 16 | s), or nullptr
 };
+
+// q8 GEMM tile: kQ8TileM rows of x by kQ8TileN weight rows, kQ8Waves waves per workgroup.
+constexpr int kQ8TileM = 64;
+constexpr int kQ8TileN = 160;
+constexpr int kQ8Waves = 4;
 
 // Cells per tile of the per-cell kernels (a) and (c).
 constexpr int kCellTile = 64;
@@ -67,6 +76,7 @@ hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s);
 hipError_t launch_contract(const ContractArgs& a, hipStream_t s);
 hipError_t launch_epilogue(const EpilogueArgs& a, int grid, hipStream_t s);
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s);
+hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st);
 hipError_t launch_q8_dequant(const uint8_t* q, const half_t* s, const half_t* b, half_t* w, int N, int K,
                              hipStream_t st);
 

@@ -1,119 +1,291 @@
 // Kernel (d): MLX-affine 8-bit weight-only linear, y = x . W^T, with
-// W[n, k] = RN_fp16(s[n, k/64] * q[n, k] + b[n, k/64]) computed by one packed
-// fp16 FMA (v_pk_fma_f16: s*q is exact, so the result is the single rounding of
-// the exact real value, the same bits as the dequantise entry point), fp32
-// accumulation on MFMA, one rounding of y to fp16.
+// W[n, k] = RN_fp16(s[n, k/64] * q[n, k] + b[n, k/64]), fp32 accumulation on
+// MFMA, one rounding of y to fp16.
 //
-// Tiling: 64 (n) x 64 (m) outputs per workgroup, K in steps of one quantisation
-// group (64). Per step the workgroup dequantises its 64x64 weight block into LDS
-// once (each thread: 16 codes, one scale/bias pair) and stages the 64x64 x block;
-// four waves (2x2) each run a 32x32 MFMA tile over the 4 k-substeps. Both LDS
-// stages are double-buffered with register prefetch one step ahead.
-// The MFMA computes y^T (rows n, columns m) so A = W and B = x are both
-// k-contiguous rows; the 4 consecutive rows of an accumulator quad are 4
-// consecutive n of one output row m: one 8-byte store.
+// Dequantisation, 3 packed instructions per 2 codes: v_perm_b32 puts a code byte
+// under the fp16 exponent of 1024 (bits 0x64qq = 1024 + q, exact), v_pk_add_f16
+// subtracts 1024 (exact: q), v_pk_fma_f16 gives RN(s*q + b) with one rounding. The
+// same bits as the dequantise entry point.
+//
+// Tiling: a workgroup owns a 64 (m) x 160 (n) tile of y = 2 x 5 blocks of the
+// 32x32x16 MFMA, and a range of K. Its 4 waves (one per SIMD) split that range into
+// contiguous runs of 64-wide groups; each wave accumulates the whole tile (10
+// independent chains) over its run, so every dequantised weight feeds 64 rows of x
+// and no two waves dequantise the same weight. Per group a lane loads 32 codes of
+// each of its 5 weight rows and 32 x values of each of its 2 x rows straight into
+// registers (one group ahead), so the main loop touches no LDS. The K order inside a
+// group is permuted (MFMA step kk takes k = 32*(lane/32) + 8*kk + e) so that a lane's
+// codes and x values are contiguous; A and B use the same order.
+// Weight codes dominate the traffic (1 byte per MAC row); M-tiles of the same n-tile
+// are neighbours in the XCD-aware order and read the codes from one L2.
+//
+// The tile's 4 partial sums meet in LDS. When K is split over several workgroups
+// (small grids: M x N too small to fill the GPU), each writes an fp32 partial to the
+// caller's workspace and a second kernel sums the partials in split order (the kernel
+// boundary orders the writes before the reads; no fences or counters): the result does
+// not depend on the order the workgroups ran in.
 #include "common.h"
 #include "kernels.h"
 
 namespace esm {
 
 namespace {
-constexpr int BN = 64;          // n per workgroup
-constexpr int BM = 64;          // m per workgroup
-constexpr int G = 64;           // quantisation group = k per step
-constexpr int KS = G + 8;       // LDS row stride (halfs)
-constexpr int WST = BN * KS;    // halfs per weight stage
-constexpr int XST = BM * KS;    // halfs per x stage
+constexpr int QG = 64;           // quantisation group: k per step
+constexpr int NBQ = 5;           // 32-row n blocks per tile
+constexpr int MBQ = 2;           // 32-row m blocks per tile
+constexpr int NWQ = 4;           // waves per workgroup
+constexpr int NBLK = MBQ * NBQ;  // accumulator blocks per tile
+static_assert(kQ8TileN == 32 * NBQ && kQ8TileM == 32 * MBQ && kQ8Waves == NWQ, "tile geometry");
 }  // namespace
 
-DEV half8 dequant8(uint32_t lo, uint32_t hi, half_t s, half_t b) {
-  // 8 codes (little-endian bytes of lo, hi) -> 8 fp16 weights s*q + b, one rounding each.
-  half8 q;
+DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
+
+// 8 codes (little-endian bytes of lo, hi) -> 8 fp16 weights RN(s*q + b).
+DEV half8 dequant8(uint32_t lo, uint32_t hi, half2v s2, half2v b2) {
+  // v_perm_b32 selector bytes 0-3 pick from the second operand (the codes), 4 picks
+  // 0x64 from the first: [q0, 0x64, q1, 0x64] is the fp16 pair (1024 + q0, 1024 + q1).
+  constexpr uint32_t kExp = 0x64646464u, kSel01 = 0x04010400u, kSel23 = 0x04030402u;
+  const uint32_t h[4] = {perm_b32(kExp, lo, kSel01), perm_b32(kExp, lo, kSel23), perm_b32(kExp, hi, kSel01),
+                         perm_b32(kExp, hi, kSel23)};
+  const half2v k1024 = {(half_t)1024.0f, (half_t)1024.0f};
+  half8 out;
 #pragma unroll
-  for (int e = 0; e < 4; e++) {
-    q[e] = (half_t)(uint16_t)((lo >> (8 * e)) & 0xffu);
-    q[e + 4] = (half_t)(uint16_t)((hi >> (8 * e)) & 0xffu);
+  for (int i = 0; i < 4; i++) {
+    const half2v qv = __builtin_bit_cast(half2v, h[i]) - k1024;  // exact
+    const half2v w = __builtin_elementwise_fma(qv, s2, b2);      // one rounding of s*q + b
+    out[2 * i] = w[0];
+    out[2 * i + 1] = w[1];
   }
-  half8 sv, bv;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    sv[e] = s;
-    bv[e] = b;
-  }
-  return __builtin_elementwise_fma(sv, q, bv);
+  return out;
 }
 
-__global__ __launch_bounds__(256, 2) void q8_linear_kernel(Q8Args p) {
-  __shared__ __align__(16) half_t w_s[2 * WST];
-  __shared__ __align__(16) half_t x_s[2 * XST];
+DEV half2v splat2(uint32_t bits) {
+  const half_t v = __builtin_bit_cast(half_t, (uint16_t)bits);
+  return half2v{v, v};
+}
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wn = wave >> 1, wm = wave & 1;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-  const int K = p.K, M = p.M, ngroups = K / G;
+// LDS stage of one step (two groups, 128 k) of a tile. Codes: 160 rows of 128 B at a
+// 136-byte stride (rows start on 32 distinct even banks: the 8-byte fragment reads of
+// 32 rows are conflict-free); x: 64 rows of 256 B at a 272-byte stride (16 rows per
+// 16-byte read pass on distinct banks); scale/bias pairs packed (b << 16 | s) per group.
+constexpr int QSTR = 136, XSTR = 272;
+constexpr int QSTAGE = kQ8TileN * QSTR, XSTAGE = kQ8TileM * XSTR, SBSTAGE = 2 * kQ8TileN * 4;
+constexpr int STAGE = QSTAGE + XSTAGE + SBSTAGE;
+constexpr int NT = NWQ * 64;
+constexpr int QCH = kQ8TileN * 8 / NT;   // 16-byte code chunks per thread per step (5)
+constexpr int XCH = kQ8TileM * 16 / NT;  // 16-byte x chunks per thread per step (4)
+constexpr int RED_BYTES = NWQ * NBLK * 4 * 64 * 16;
+static_assert(kQ8TileN * 8 % NT == 0 && kQ8TileM * 16 % NT == 0 && kQ8TileN <= NT, "loader split");
+static_assert(2 * STAGE <= RED_BYTES, "stages fit in the reduction area");
 
-  // Weight loader: thread -> (row n0 + tid/4, 16 codes at k = 16*(tid%4)).
-  const int wrow = tid >> 2, wpart = tid & 3;
-  const uint8_t* qrow = p.q + (size_t)(n0 + wrow) * K + wpart * 16;
-  const half_t* srow = p.s + (size_t)(n0 + wrow) * ngroups;
-  const half_t* brow = p.b + (size_t)(n0 + wrow) * ngroups;
-  // x loader: 2 chunks of 8 halfs per thread.
-  u32x4 qpre;
-  half_t spre, bpre;
-  half8 xpre[2];
+// One step's global loads of one thread (registers, issued a step ahead of their LDS store).
+struct Q8Load {
+  u32x4 q[QCH];
+  u32x4 x[XCH];
+  u32x4 sbv;                  // packed scales: 4 (b << 16 | s) words of the step's 320
+  uint32_t s0, s1, b0, b1;    // unpacked: one row's two groups
+};
+constexpr int SBT = 2 * kQ8TileN / 4;  // threads that load a step's packed scale words
 
-  auto gload = [&](int kg) {
-    qpre = *reinterpret_cast<const u32x4*>(qrow + (size_t)kg * G);
-    spre = srow[kg];
-    bpre = brow[kg];
+// PACKED: scales and biases come pre-packed per tile ([n-tile][group][160] words of
+// b << 16 | s, from q8_pack_scales): a step's 320 words are 1280 contiguous bytes, one
+// 16-byte load for 80 threads. Unpacked, every thread of the first 160 reads its row's
+// fp16 pairs from the [N, K/64] arrays: 160 scattered rows per step, several times the
+// L1 requests of the codes and x together.
+template <bool PACKED>
+__global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
+  __shared__ __align__(16) char smem[RED_BYTES];  // two step stages, then every wave's partial tile
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, kg = lane >> 5;
+
+  // Logical order: n-tile, then split, then m-tile fastest (XCD neighbours share codes).
+  int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int mt = t % p.mtiles;
+  t /= p.mtiles;
+  const int sp = t % p.splits;
+  const int nt = t / p.splits;
+  const int m0 = mt * kQ8TileM, n0 = nt * kQ8TileN;
+  const int K = p.K, M = p.M, N = p.N, ngroups = K / QG;
+  // This split's groups [sg0, sg1), walked two at a time.
+  const int sg0 = (int)((long long)ngroups * sp / p.splits);
+  const int sg1 = (int)((long long)ngroups * (sp + 1) / p.splits);
+  const int nsteps = (sg1 - sg0 + 1) / 2;
+
+  // Buffer ranges end exactly at the arrays' ends: rows past M or N load zeros. The
+  // second group of a step past sg1 (odd group count) loads zeros for x, so it adds 0.
+  const rsrc_t rq = make_rsrc_n(p.q + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
+  const rsrc_t rs = make_rsrc_n(p.s + (size_t)n0 * ngroups, (uint32_t)(N - n0) * (uint32_t)ngroups * 2u);
+  const rsrc_t rb = make_rsrc_n(p.b + (size_t)n0 * ngroups, (uint32_t)(N - n0) * (uint32_t)ngroups * 2u);
+  const rsrc_t rx = make_rsrc_n(p.x + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K * 2u);
+  const rsrc_t rsb = make_rsrc_n(PACKED ? (const void*)(p.sb + (size_t)nt * ngroups * kQ8TileN) : (const void*)p.x,
+                                 PACKED ? (uint32_t)ngroups * kQ8TileN * 4u : 0u);
+
+  // Coalesced loads: 8 lanes per 128-byte code row piece, 16 lanes per 256-byte x row piece.
+  auto gload = [&](Q8Load& ld, int step) {
+    const int g = sg0 + 2 * step;
+    const bool two = g + 1 < sg1;
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const int id = tid + 256 * u;
-      const int row = id >> 3, kc = id & 7;
-      xpre[u] = (m0 + row < M) ? ld16(p.x + (size_t)(m0 + row) * K + (size_t)kg * G + kc * 8) : zero_half8();
+    for (int i = 0; i < QCH; i++) {
+      const int c = tid + NT * i, row = c >> 3, j = c & 7;
+      ld.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)((uint32_t)row * K + g * QG + 16 * j), 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < XCH; i++) {
+      const int c = tid + NT * i, row = c >> 4, j = c & 15;
+      const uint32_t off = (j < 8 || two) ? ((uint32_t)row * K + g * QG) * 2u + 16u * j : kOOB;
+      ld.x[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+    }
+    if (PACKED) {
+      ld.sbv = __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(tid < SBT ? ((uint32_t)g * kQ8TileN + 4u * tid) * 4u : kOOB),
+                                                     0, 0);
+    } else {
+      const uint32_t so = tid < kQ8TileN ? ((uint32_t)tid * ngroups + g) * 2u : kOOB;
+      ld.s0 = bload2(rs, so);
+      ld.s1 = bload2(rs, so + 2u);
+      ld.b0 = bload2(rb, so);
+      ld.b1 = bload2(rb, so + 2u);
     }
   };
-  auto swrite = [&](int buf) {
-    half_t* wd = w_s + buf * WST + wrow * KS + wpart * 16;
-    st16(wd, dequant8(qpre[0], qpre[1], spre, bpre));
-    st16(wd + 8, dequant8(qpre[2], qpre[3], spre, bpre));
+  auto sstore = [&](const Q8Load& ld, int buf) {
+    char* st = smem + buf * STAGE;
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const int id = tid + 256 * u;
-      const int row = id >> 3, kc = id & 7;
-      st16(x_s + buf * XST + row * KS + kc * 8, xpre[u]);
+    for (int i = 0; i < QCH; i++) {
+      const int c = tid + NT * i, row = c >> 3, j = c & 7;
+      u32x2* d = reinterpret_cast<u32x2*>(st + row * QSTR + 16 * j);  // 8-byte aligned rows
+      d[0] = u32x2{ld.q[i][0], ld.q[i][1]};
+      d[1] = u32x2{ld.q[i][2], ld.q[i][3]};
+    }
+#pragma unroll
+    for (int i = 0; i < XCH; i++) {
+      const int c = tid + NT * i, row = c >> 4, j = c & 15;
+      *reinterpret_cast<u32x4*>(st + QSTAGE + row * XSTR + 16 * j) = ld.x[i];
+    }
+    uint32_t* sb = reinterpret_cast<uint32_t*>(st + QSTAGE + XSTAGE);
+    if (PACKED) {
+      if (tid < SBT) *reinterpret_cast<u32x4*>(sb + 4 * tid) = ld.sbv;
+    } else if (tid < kQ8TileN) {
+      sb[tid] = (ld.b0 << 16) | (ld.s0 & 0xffffu);
+      sb[kQ8TileN + tid] = (ld.b1 << 16) | (ld.s1 & 0xffffu);
     }
   };
 
-  f32x16 acc;
+  f32x16 acc[MBQ][NBQ];
 #pragma unroll
-  for (int r = 0; r < 16; r++) acc[r] = 0.f;
+  for (int mb = 0; mb < MBQ; mb++)
+#pragma unroll
+    for (int nb = 0; nb < NBQ; nb++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[mb][nb][i] = 0.f;
 
-  gload(0);
-  swrite(0);
-  __syncthreads();
-  for (int kg = 0; kg < ngroups; kg++) {
-    const int buf = kg & 1;
-    if (kg + 1 < ngroups) gload(kg + 1);
-    const half_t* ws = w_s + buf * WST + (wn * 32 + (lane & 31)) * KS + 8 * (lane >> 5);
-    const half_t* xs = x_s + buf * XST + (wm * 32 + (lane & 31)) * KS + 8 * (lane >> 5);
+  // Wave w takes MFMA step kk = w (k = 16 w .. 16 w + 15) of both groups of a step:
+  // D[n][m] += W[n][k] x[m][k], A = dequantised codes (row n = lane%32), B = x.
+  auto compute = [&](int buf) {
+    const char* st = smem + buf * STAGE;
+    const uint32_t* sb = reinterpret_cast<const uint32_t*>(st + QSTAGE + XSTAGE);
 #pragma unroll
-    for (int kk = 0; kk < G / 16; kk++) acc = mfma32(ld16(ws + kk * 16), ld16(xs + kk * 16), acc);
-    if (kg + 1 < ngroups) swrite(buf ^ 1);
+    for (int g = 0; g < 2; g++) {
+      half8 a[NBQ];
+#pragma unroll
+      for (int nb = 0; nb < NBQ; nb++) {
+        const int row = 32 * nb + r;
+        const uint32_t w = sb[g * kQ8TileN + row];
+        const u32x2 c = *reinterpret_cast<const u32x2*>(st + row * QSTR + 64 * g + 16 * wave + 8 * kg);
+        a[nb] = dequant8(c[0], c[1], splat2(w & 0xffffu), splat2(w >> 16));
+      }
+      half8 xf[MBQ];
+#pragma unroll
+      for (int mb = 0; mb < MBQ; mb++)
+        xf[mb] = *reinterpret_cast<const half8*>(st + QSTAGE + (32 * mb + r) * XSTR + 128 * g + 32 * wave + 16 * kg);
+#pragma unroll
+      for (int nb = 0; nb < NBQ; nb++)
+#pragma unroll
+        for (int mb = 0; mb < MBQ; mb++) acc[mb][nb] = mfma32(a[nb], xf[mb], acc[mb][nb]);
+    }
+  };
+
+  // Pipeline: step s+2's loads in flight while step s computes from LDS and step s+1's
+  // registers wait to be stored; one barrier per step. Unrolled by two (register sets
+  // A and B), a single loop exit, the leftover step after it.
+  Q8Load la, lb;
+  if (nsteps > 0) {
+    gload(la, 0);
+    gload(lb, 1);
+    sstore(la, 0);
     __syncthreads();
   }
+  int st = 0;
+  for (; st + 2 <= nsteps; st += 2) {
+    gload(la, st + 2);
+    compute(0);
+    sstore(lb, 1);
+    __syncthreads();
+    gload(lb, st + 3);
+    compute(1);
+    sstore(la, 0);
+    __syncthreads();
+  }
+  if (st < nsteps) compute(0);
+  __syncthreads();  // the stages are reused as the reduction area
 
-  // acc rows are n, columns are m: 4 consecutive n per register quad.
-  const int m = m0 + wm * 32 + (lane & 31);
-  if (m < M) {
+  // The 4 partial tiles -> LDS; wave w then finishes blocks w, w+4, w+8.
+  f32x4 (*red)[NBLK][4][64] = reinterpret_cast<f32x4 (*)[NBLK][4][64]>(smem);
+#pragma unroll
+  for (int mb = 0; mb < MBQ; mb++)
+#pragma unroll
+    for (int nb = 0; nb < NBQ; nb++)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++)
+        red[wave][mb * NBQ + nb][r4][lane] =
+            f32x4{acc[mb][nb][4 * r4], acc[mb][nb][4 * r4 + 1], acc[mb][nb][4 * r4 + 2], acc[mb][nb][4 * r4 + 3]};
+  __syncthreads();
+
+  // Lane's output coordinates in block blk: column m = lane%32, rows n = 4 consecutive per r4.
+  auto tile_sum = [&](int blk, int r4) {
+    f32x4 v = red[0][blk][r4][lane];
+#pragma unroll
+    for (int w = 1; w < NWQ; w++) v += red[w][blk][r4][lane];
+    return v;
+  };
+  const int tile_id = nt * p.mtiles + mt;
+  if (p.splits == 1) {
+    for (int blk = wave; blk < NBLK; blk += NWQ) {
+      const int mb = blk / NBQ, nb = blk - mb * NBQ;
+      const int m = m0 + 32 * mb + r;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++) {
+        const int n = n0 + 32 * nb + acc_row32(4 * r4, lane);
+        const f32x4 v = tile_sum(blk, r4);
+        if (m < M && n < N)
+          *reinterpret_cast<half4*>(p.y + (size_t)m * N + n) = half4{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+      }
+    }
+    return;
+  }
+
+  // Split K: this workgroup's fp32 partial; q8_reduce_kernel sums the splits.
+  float* part = p.part + (size_t)sp * M * N;
+  for (int blk = wave; blk < NBLK; blk += NWQ) {
+    const int mb = blk / NBQ, nb = blk - mb * NBQ;
+    const int m = m0 + 32 * mb + r;
 #pragma unroll
     for (int r4 = 0; r4 < 4; r4++) {
-      const int n = n0 + wn * 32 + acc_row32(4 * r4, lane);
-      half4 v;
-#pragma unroll
-      for (int e = 0; e < 4; e++) v[e] = (half_t)acc[4 * r4 + e];
-      *reinterpret_cast<half4*>(p.y + (size_t)m * p.N + n) = v;
+      const int n = n0 + 32 * nb + acc_row32(4 * r4, lane);
+      const f32x4 v = tile_sum(blk, r4);
+      if (m < M && n < N) *reinterpret_cast<f32x4*>(part + (size_t)m * N + n) = v;
     }
+  }
+}
+
+// y = sum of the split partials in split order (deterministic), one rounding to fp16.
+// Four outputs per thread; M * N is a multiple of 64.
+__global__ __launch_bounds__(256) void q8_reduce_kernel(const float* __restrict__ part, half_t* __restrict__ y,
+                                                        size_t n4, size_t plane, int splits) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+    f32x4 v = reinterpret_cast<const f32x4*>(part)[i];
+    for (int s = 1; s < splits; s++) v += reinterpret_cast<const f32x4*>(part + (size_t)s * plane)[i];
+    reinterpret_cast<half4*>(y)[i] = half4{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
   }
 }
 
@@ -125,15 +297,47 @@ __global__ __launch_bounds__(256) void q8_dequant_kernel(const uint8_t* __restri
     const size_t e0 = c * 16;
     const size_t n = e0 / K;
     const size_t k = e0 - n * K;
-    const size_t gi = n * (K / G) + k / G;
+    const size_t gi = n * (K / QG) + k / QG;
     const u32x4 v = *reinterpret_cast<const u32x4*>(q + e0);
-    st16(w + e0, dequant8(v[0], v[1], s[gi], b[gi]));
-    st16(w + e0 + 8, dequant8(v[2], v[3], s[gi], b[gi]));
+    const half2v s2 = splat2(__builtin_bit_cast(uint16_t, s[gi])), b2 = splat2(__builtin_bit_cast(uint16_t, b[gi]));
+    st16(w + e0, dequant8(v[0], v[1], s2, b2));
+    st16(w + e0 + 8, dequant8(v[2], v[3], s2, b2));
   }
 }
 
+// sb[(t * ngroups + g) * 160 + j] = b[n, g] << 16 | s[n, g] for n = 160 t + j (0 past N).
+__global__ __launch_bounds__(256) void q8_pack_kernel(const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
+                                                      uint32_t* __restrict__ sb, int N, int ngroups, size_t total) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int j = (int)(i % kQ8TileN);
+    const size_t rest = i / kQ8TileN;
+    const int g = (int)(rest % ngroups);
+    const int n = (int)(rest / ngroups) * kQ8TileN + j;
+    sb[i] = n < N ? ((uint32_t)b[(size_t)n * ngroups + g] << 16) | s[(size_t)n * ngroups + g] : 0u;
+  }
+}
+
+hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st) {
+  const int ngroups = K / QG, ntiles = (N + kQ8TileN - 1) / kQ8TileN;
+  const size_t total = (size_t)ntiles * ngroups * kQ8TileN;
+  const size_t blocks = (total + 255) / 256;
+  hipLaunchKernelGGL(q8_pack_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st,
+                     reinterpret_cast<const uint16_t*>(s), reinterpret_cast<const uint16_t*>(b), sb, N, ngroups, total);
+  return hipGetLastError();
+}
+
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s) {
-  hipLaunchKernelGGL(q8_linear_kernel, dim3(a.N / BN, (a.M + BM - 1) / BM), dim3(256), 0, s, a);
+  const int grid = a.mtiles * a.ntiles * a.splits;
+  if (a.sb)
+    hipLaunchKernelGGL(q8_linear_kernel<true>, dim3(grid), dim3(NWQ * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL(q8_linear_kernel<false>, dim3(grid), dim3(NWQ * 64), 0, s, a);
+  if (a.splits > 1) {
+    const size_t plane = (size_t)a.M * a.N, n4 = plane / 4;
+    const size_t blocks = (n4 + 255) / 256;
+    hipLaunchKernelGGL(q8_reduce_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, s, a.part, a.y,
+                       n4, plane, a.splits);
+  }
   return hipGetLastError();
 }
 

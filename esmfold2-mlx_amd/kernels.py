@@ -88,8 +88,38 @@ def epilogue(x, z, mask, ln_in_w, ln_in_b, eps_in, ln_mix_w, ln_mix_b, eps_mix, 
     return out
 
 
-def q8_linear(x, q, s, b, group: int = 64, out=None):
-    """Kernel (d): y = x . W^T, W = s*q + b per group of 64 along K (fp16 in/out, fp32 accumulation)."""
+def q8_workspace_bytes(M: int, K: int, N: int) -> int:
+    """Bytes of workspace q8_linear uses to split K at this shape (0: it runs unsplit)."""
+    return int(capi.lib().q8_linear_workspace_bytes(M, K, N))
+
+
+def q8_workspace(M: int, K: int, N: int, device=None):
+    """A workspace for q8_linear at this shape, or None when it needs none. Reusable across
+    calls of that shape on one stream, not by calls that overlap in time."""
+    n = q8_workspace_bytes(M, K, N)
+    if n == 0:
+        return None
+    return torch.empty(n + 256, dtype=torch.uint8, device=device if device is not None else "cuda")
+
+
+def q8_pack_scales(s, b, group: int = 64):
+    """Scales and biases [N, K/64] fp16 packed as q8_linear's per-tile words (a layout cache)."""
+    lib = capi.lib()
+    _dev(s, "s", F16)
+    _dev(b, "b", F16)
+    N, G = s.shape
+    if b.shape != s.shape:
+        raise capi.EsmError(-2, f"q8_pack_scales: s{tuple(s.shape)} b{tuple(b.shape)}")
+    n = int(lib.q8_packed_scales_bytes(N, G * group))
+    sb = torch.empty(n // 4, dtype=torch.int32, device=s.device)
+    capi.check(lib.q8_pack_scales(s.data_ptr(), b.data_ptr(), sb.data_ptr(), N, G * group, group, capi.stream_ptr()))
+    return sb
+
+
+def q8_linear(x, q, s, b, group: int = 64, out=None, workspace=None, packed=None):
+    """Kernel (d): y = x . W^T, W = s*q + b per group of 64 along K (fp16 in/out, fp32 accumulation).
+    ``packed`` (from ``q8_pack_scales``) and ``workspace`` (from ``q8_workspace``) are optional
+    speed-ups; the result is the same bits with or without them."""
     lib = capi.lib()
     _dev(x, "x", F16)
     _dev(q, "q", torch.uint8)
@@ -100,8 +130,20 @@ def q8_linear(x, q, s, b, group: int = 64, out=None):
     if q.shape[1] != K or s.shape != (N, K // group) or b.shape != s.shape:
         raise capi.EsmError(-2, f"q8_linear: shapes x{tuple(x.shape)} q{tuple(q.shape)} s{tuple(s.shape)}")
     y = torch.empty(M, N, dtype=F16, device=x.device) if out is None else _dev(out, "out", F16)
-    capi.check(lib.q8_linear(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), y.data_ptr(), M, K, N, group,
-                             capi.stream_ptr()))
+    if workspace is None:
+        wp, wn = None, 0
+    else:
+        _dev(workspace, "workspace", torch.uint8)
+        wp = (workspace.data_ptr() + 255) // 256 * 256
+        wn = workspace.numel() - (wp - workspace.data_ptr())
+    sbp = None
+    if packed is not None:
+        _dev(packed, "packed", torch.int32)
+        if packed.numel() * 4 < lib.q8_packed_scales_bytes(N, K):
+            raise capi.EsmError(-2, "q8_linear: packed scales too small for this shape")
+        sbp = packed.data_ptr()
+    capi.check(lib.q8_linear_ws(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), sbp, y.data_ptr(), M, K, N,
+                                group, wp, wn, capi.stream_ptr()))
     return y
 
 

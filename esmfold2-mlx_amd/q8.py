@@ -6,7 +6,9 @@ input axis of torch's [out, in] layout with fp16 scales and biases
 (mlx_esmc.py:53-75). ``Q8Linear`` takes the same three arrays (codes as uint8
 [N, K], which is the little-endian byte view of MLX's uint32 packing) and
 computes y = x . W^T with W = s*q + b on the gfx950 kernel: fp16 activations,
-fp32 accumulation, fp16 output.
+fp32 accumulation, fp16 output. The scales and biases are packed once per layer
+into the kernel's per-tile layout, and shapes whose output tiles cannot fill the
+GPU get a per-M workspace (allocated once) so K is split over more workgroups.
 """
 
 from __future__ import annotations
@@ -30,6 +32,8 @@ class Q8Linear(nn.Module):
         self.register_buffer("scales", scales.detach().to(device=dev, dtype=torch.float16).contiguous())
         self.register_buffer("biases", biases.detach().to(device=dev, dtype=torch.float16).contiguous())
         self.in_features, self.out_features = K, N
+        self.register_buffer("packed", kernels.q8_pack_scales(self.scales, self.biases, GROUP))
+        self._ws = {}  # rows M -> split-K workspace (None: the shape runs unsplit)
 
     @classmethod
     def from_packed_u32(cls, w_u32: torch.Tensor, scales, biases, **kw) -> "Q8Linear":
@@ -46,6 +50,9 @@ class Q8Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
-        y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP)
+        M = x2.shape[0]
+        if M not in self._ws:
+            self._ws[M] = kernels.q8_workspace(M, self.in_features, self.out_features, device=x2.device)
+        y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP, workspace=self._ws[M], packed=self.packed)
         y = y.reshape(*lead, self.out_features)
         return y if x.dtype == torch.float16 else y.to(x.dtype)

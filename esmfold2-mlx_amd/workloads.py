@@ -1,0 +1,73 @@
+"""Seeded synthetic workloads of the benchmark configurations (generated on the CPU).
+
+There are no checkpoints, so the benchmark, the smoke run and the tests use the same
+seeded draws; both sides of a comparison see identical bytes.
+
+* ``pair_inputs``: a pair tensor z [B, L, L, C] ~ N(0, 1), then the outgoing and the
+  incoming update's weights: proj_bundle.weight [4c, C], proj_gate.weight [C, C],
+  proj_emit.weight [C, c], in that order, each N(0, 1/fan_in); LayerNorm gamma = 1,
+  beta = 0 (no draws). fp32 master weights; z cast to ``dtype`` after the fp32 draw.
+* ``q8_inputs``: x [M, K] fp16 ~ N(0, 1); codes q [N, K] ~ U{0..255}; scales
+  s [N, K/64] ~ U(0.001, 0.01) and biases b ~ N(0, 0.1), fp16; drawn in that order.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+EPS = 1e-5
+
+
+@dataclass
+class TriMulParams:
+    """One triangle multiplicative update's weights in torch's [out, in] layout: the
+    attributes ``TriMul.from_weights`` reads (the reference's TriangleMultiplicativeBlock
+    fields, fast_trunk.py:53-56)."""
+
+    w_bundle: torch.Tensor   # [4c, C], rows [s_a | s_b | g_a | g_b]
+    w_emit: torch.Tensor     # [C, c]
+    w_gate: torch.Tensor     # [C, C]
+    ln_in_w: torch.Tensor    # [C]
+    ln_in_b: torch.Tensor    # [C]
+    ln_mix_w: torch.Tensor   # [c]
+    ln_mix_b: torch.Tensor   # [c]
+    outgoing: bool = True
+    ln_in_eps: float = EPS
+    ln_mix_eps: float = EPS
+
+
+def tmu_params(gen: torch.Generator, C: int, c: int, outgoing: bool) -> TriMulParams:
+    f32 = torch.float32
+    w = torch.randn(4 * c, C, generator=gen, dtype=f32) * (1.0 / C) ** 0.5
+    wg = torch.randn(C, C, generator=gen, dtype=f32) * (1.0 / C) ** 0.5
+    we = torch.randn(C, c, generator=gen, dtype=f32) * (1.0 / c) ** 0.5
+    return TriMulParams(w_bundle=w, w_emit=we, w_gate=wg, ln_in_w=torch.ones(C, dtype=f32),
+                        ln_in_b=torch.zeros(C, dtype=f32), ln_mix_w=torch.ones(c, dtype=f32),
+                        ln_mix_b=torch.zeros(c, dtype=f32), outgoing=outgoing)
+
+
+def pair_inputs(L: int, C: int = 128, c: int = 128, seed: int = 0, dtype=torch.float16, B: int = 1,
+                pad_from: int | None = None):
+    """(z, mask, outgoing params, incoming params); mask m[i,j] = (i < pad_from)(j < pad_from)
+    as [B, L, L] fp32, or None."""
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn(B, L, L, C, generator=g, dtype=torch.float32).to(dtype)
+    p_out = tmu_params(g, C, c, True)
+    p_in = tmu_params(g, C, c, False)
+    mask = None
+    if pad_from is not None:
+        v = (torch.arange(L) < pad_from).to(torch.float32)
+        mask = (v[:, None] * v[None, :]).expand(B, L, L).contiguous()
+    return z, mask, p_out, p_in
+
+
+def q8_inputs(M: int, K: int, N: int, seed: int = 0, group: int = 64):
+    """(x fp16 [M, K], q uint8 [N, K], s fp16 [N, K/group], b fp16 [N, K/group]) on the CPU."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g, dtype=torch.float32).half()
+    q = torch.randint(0, 256, (N, K), generator=g, dtype=torch.int64).to(torch.uint8)
+    s = (torch.rand(N, K // group, generator=g, dtype=torch.float32) * 0.009 + 0.001).half()
+    b = (torch.randn(N, K // group, generator=g, dtype=torch.float32) * 0.1).half()
+    return x, q, s, b

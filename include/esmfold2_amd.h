@@ -159,6 +159,35 @@ int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_
               int N, int group, void* stream);
 
 /*
+ * q8_linear with the two optional speed-ups a long-lived caller (a layer holding its
+ * weights) can afford:
+ *   sb: the scales and biases pre-packed by q8_pack_scales (once per weight matrix);
+ *       NULL reads them from s and b (slower: 160 scattered rows per 128-wide step).
+ *   workspace: for shapes whose output tiles (64 x 160) are too few to fill the GPU
+ *       (e.g. M = 238, N = 2560), K is split over several workgroups whose fp32
+ *       partials go through the workspace and are summed in split order by a second
+ *       kernel on the same stream (deterministic). q8_linear_workspace_bytes(M, K, N)
+ *       bytes, 256-byte aligned, no initialisation needed; NULL runs unsplit. Calls
+ *       that share a workspace must not overlap in time.
+ * s and b are required either way. Same semantics and result as q8_linear
+ * (mx.quantized_matmul, mlx_esmc.py:78-81); packed or not, the bits are identical.
+ */
+int q8_linear_ws(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, const uint32_t* sb,
+                 esm_half* y, int M, int K, int N, int group, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes q8_linear_ws uses for this shape on the current device (0: none). */
+size_t q8_linear_workspace_bytes(int M, int K, int N);
+
+/*
+ * Packs s and b [N, K/group] fp16 into sb [ceil(N/160), K/group, 160] uint32 words
+ * (b << 16 | s; rows past N are 0), the layout q8_linear_ws reads a step of in one
+ * coalesced load. A layout cache of the reference's fp16 scales/biases
+ * (mlx_esmc.py:53-75), built once per weight matrix. group = 64.
+ */
+size_t q8_packed_scales_bytes(int N, int K);
+int q8_pack_scales(const esm_half* s, const esm_half* b, uint32_t* sb, int N, int K, int group, void* stream);
+
+/*
  * Dequantise only: w[n, k] = RN_fp16(s[n, k/group] * q[n, k] + b[n, k/group]),
  * the exact weights q8_linear multiplies by (for the bit-exact check).
  * q [N, K] uint8; s, b [N, K/group] fp16; w [N, K] fp16. group = 64, K % 64 == 0.

@@ -24,8 +24,8 @@ def lib(pkg):
 
 def test_header_declares_the_entry_points():
     names = declared_functions()
-    for n in ("tmu_project", "tmu_contract", "tmu_epilogue", "tmu_forward", "q8_linear", "q8_dequant",
-              "esm_last_error", "esm_version", "tmu_workspace_bytes", "tmu_leading_dim"):
+    for n in ("tmu_project", "tmu_contract", "tmu_epilogue", "tmu_forward", "q8_linear", "q8_linear_ws",
+              "q8_linear_workspace_bytes", "q8_pack_scales", "q8_packed_scales_bytes", "q8_dequant", "esm_last_error", "esm_version", "tmu_workspace_bytes", "tmu_leading_dim"):
         assert n in names
 
 
@@ -65,6 +65,20 @@ def test_rejects_null_and_bad_shapes(lib):
     assert lib.q8_linear(None, None, None, None, None, 4, 100, 64, 64, None) == -2  # K % 64
     assert lib.q8_linear(None, None, None, None, None, 4, 128, 64, 32, None) == -4  # group 32
     assert lib.q8_dequant(None, None, None, None, 64, 64, 64, None) == -1
+    assert lib.q8_linear_ws(None, None, None, None, None, None, 5, 1024, 64, 64, None, 0, None) == -1
+    assert lib.q8_pack_scales(None, None, None, 64, 128, 64, None) == -1
+    assert lib.q8_pack_scales(None, None, None, 64, 100, 64, None) == -2
+    assert lib.q8_packed_scales_bytes(64, 128) == 1 * 2 * 160 * 4 and lib.q8_packed_scales_bytes(161, 64) == 2 * 160 * 4
+    # split-K workspace: too small, then misaligned (both rejected before any launch)
+    need = lib.q8_linear_workspace_bytes(5, 1024, 64)
+    assert need > 0 and lib.q8_linear_workspace_bytes(238, 2560, 10240) == 0
+    assert lib.q8_linear_workspace_bytes(5, 100, 64) == 0  # unsupported K
+    ws = ctypes.c_void_p(1 << 20)
+    assert lib.q8_linear_ws(fake16 := ctypes.c_void_p(4096), fake16, fake16, fake16, None, fake16, 5, 1024, 64, 64,
+                            ws, need - 1, None) == -2
+    assert "workspace" in _err(lib)
+    assert lib.q8_linear_ws(fake16, fake16, fake16, fake16, None, fake16, 5, 1024, 64, 64,
+                            ctypes.c_void_p((1 << 20) + 16), need, None) == -3
     # misaligned leading dimension (not a multiple of 8): checked before any pointer is used
     fake = ctypes.c_void_p(4096)
     assert lib.tmu_contract(fake, fake, fake, 1, 10, 12, 16, 1.0, None) == -2

@@ -85,3 +85,65 @@ def test_q8_linear_rejects_bad_shapes(gpu_lib, pkg):
     x, q, s, b = q8.make_q8_inputs(4, 128, 64, seed=0)
     with pytest.raises(Exception):
         pkg.kernels.q8_linear(_t(x[:, :64]), _t(q), _t(s), _t(b))
+
+
+@pytest.mark.parametrize("M,K,N", [(238, 10240, 2560), (5, 1024, 64), (64, 4096, 320), (130, 512, 192)])
+def test_q8_linear_split_k(gpu_lib, pkg, M, K, N):
+    # shapes whose 64 x 160 output tiles cannot fill the GPU split K over workgroups through
+    # the workspace; the last workgroup of a tile sums the fp32 partials in split order
+    nbytes = pkg.kernels.q8_workspace_bytes(M, K, N)
+    assert nbytes > 0, "this shape is expected to split K"
+    ws = pkg.kernels.q8_workspace(M, K, N)
+    x, q, s, b = q8.make_q8_inputs(M, K, N, seed=M + K)
+    x2 = np.random.default_rng(1).standard_normal((M, K)).astype(np.float16)
+    args = (_t(q), _t(s), _t(b))
+    y1 = pkg.kernels.q8_linear(_t(x), *args, workspace=ws).cpu().numpy()
+    _check(y1, x, q, s, b)
+    # the workspace is left ready: a second call (other x) and a repeat of the first
+    y2 = pkg.kernels.q8_linear(_t(x2), *args, workspace=ws).cpu().numpy()
+    _check(y2, x2, q, s, b)
+    y3 = pkg.kernels.q8_linear(_t(x), *args, workspace=ws).cpu().numpy()
+    assert np.array_equal(y1.view(np.uint16), y3.view(np.uint16)), "split-K result depends on arrival order"
+    # the unsplit kernel (no workspace) agrees to the accumulation-order bound
+    y0 = pkg.kernels.q8_linear(_t(x), *args).cpu().numpy()
+    _check(y0, x, q, s, b)
+
+
+def test_q8_workspace_sizes_and_errors(gpu_lib, pkg):
+    assert pkg.kernels.q8_workspace_bytes(238, 2560, 10240) == 0  # 256 tiles: no split
+    M, K, N = 5, 1024, 64
+    x, q, s, b = q8.make_q8_inputs(M, K, N, seed=2)
+    small = torch.zeros(64 + 256, dtype=torch.uint8, device=DEV)
+    with pytest.raises(pkg.capi.EsmError):
+        pkg.kernels.q8_linear(_t(x), _t(q), _t(s), _t(b), workspace=small)
+
+
+def test_q8_module_split_k_workspace(gpu_lib, pkg):
+    # the module keeps one workspace per row count and reuses it
+    x, q, s, b = q8.make_q8_inputs(238, 4096, 640, seed=9)
+    lin = pkg.q8.Q8Linear(torch.from_numpy(q), torch.from_numpy(s), torch.from_numpy(b))
+    xt = torch.from_numpy(x).to(DEV)
+    y = lin(xt)
+    assert lin._ws[238] is not None
+    _check(y.cpu().numpy(), x, q, s, b)
+    _check(lin(xt).cpu().numpy(), x, q, s, b)
+
+
+@pytest.mark.parametrize("M,K,N", [(238, 2560, 640), (238, 10240, 320), (7, 192, 192)])
+def test_q8_packed_scales_same_bits(gpu_lib, pkg, M, K, N):
+    # the packed-scale layout is a cache: same bits as the [N, K/64] arrays, split or not
+    x, q, s, b = (_t(a) for a in q8.make_q8_inputs(M, K, N, seed=N))
+    sb = pkg.kernels.q8_pack_scales(s, b)
+    # layout: word (t, g, j) = b[160 t + j, g] << 16 | s[160 t + j, g], 0 past N
+    s16, b16 = s.cpu().numpy().view(np.uint16), b.cpu().numpy().view(np.uint16)
+    T, G = -(-N // 160), K // 64
+    ref = np.zeros((T, G, 160), dtype=np.uint32)
+    for t in range(T):
+        rows = np.arange(160 * t, min(160 * t + 160, N))
+        ref[t, :, :len(rows)] = (b16[rows].astype(np.uint32).T << 16) | s16[rows].astype(np.uint32).T
+    assert np.array_equal(sb.cpu().numpy().view(np.uint32).reshape(T, G, 160), ref)
+    ws = pkg.kernels.q8_workspace(M, K, N)
+    y_plain = pkg.kernels.q8_linear(x, q, s, b, workspace=ws)
+    y_packed = pkg.kernels.q8_linear(x, q, s, b, workspace=ws, packed=sb)
+    assert torch.equal(y_plain.view(torch.int16), y_packed.view(torch.int16))
+    _check(y_packed.cpu().numpy(), *q8.make_q8_inputs(M, K, N, seed=N))
