@@ -11,6 +11,10 @@ Also reported on the same JSON line:
   kernels       the same figures for every kernel of the step;
   q8            the 8-bit ESMC-style linears [238,2560]x[2560->10240] and
                 [238,10240]x[10240->2560] (time, TFLOP/s, GB/s);
+  transition    the pair transition kernel (LN -> 128->512 -> ReLU -> 512->128 + z)
+                at L=238 (time, TFLOP/s, fraction of MFMA peak);
+  block_stack   the pair-trunk block stack at L=238: 8 blocks of (T_out, T_in,
+                transition) x 3 recycles with z carried, replayed as one HIP graph;
   cpu_baseline  the CPU oracle (torch fp32 restatement of the reference's
                 _trimul_forward) on the host cores, a bounded sample of the same
                 workload (rank 0, N=1 only). This leg is also the checker: the
@@ -72,6 +76,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-q8", action="store_true", help="skip the q8 linear figures")
+    ap.add_argument("--no-stack", action="store_true", help="skip the transition and block-stack figures")
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 64 MiB device copy 10 times (counter calibration under rocprofv3)")
@@ -89,7 +94,7 @@ def copy_probe(dev, reps: int = 10, nbytes: int = 64 << 20):
     torch.cuda.synchronize()
 
 
-def cpu_baseline(z, po, pi, pair_out, q8_samples):
+def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None):
     """The CPU oracle in fp32 on the host cores: 1 warm-up, median of 3 TMU pairs at L=238.
     Also the checker of the GPU leg: the benchmarked pair output against the oracle's
     (max|err| / RMS(update), bar 1e-2) and the sampled q8 rows (normwise, bar 1e-3)."""
@@ -117,10 +122,27 @@ def cpu_baseline(z, po, pi, pair_out, q8_samples):
         yr = oq8.q8_linear(x[rows].numpy(), q.numpy(), s.numpy(), b.numpy())
         q8_err[name] = float(np.linalg.norm(y - yr) / np.linalg.norm(yr))
     ok = pair_err <= 1e-2 and all(e <= 1e-3 for e in q8_err.values())
+    stack_err = None
+    if stack_case is not None:
+        # the block stack against the oracle with an fp16 residual stream (fp32, CPU)
+        from oracle import transition as otr
+        zs, blocks, got = stack_case
+        ob = [otr.BlockWeights(tmu.TriMulWeights(**{f: getattr(a, f) for f in fields}),
+                               tmu.TriMulWeights(**{f: getattr(b, f) for f in fields}),
+                               otr.TransitionWeights(t.ln_w, t.ln_b, t.w1, t.w3, t.w2, eps=t.eps))
+              for a, b, t in blocks]
+        with torch.no_grad():
+            ref = otr.stack_forward(zs.float(), None, ob, 3, store=torch.float16).double()
+        u = ref - zs.double()
+        d = got.double() - ref
+        rms = float(u.pow(2).mean().sqrt())
+        stack_err = {"max_err_over_rms": float(d.abs().max()) / rms, "rms_err_over_rms": float(d.pow(2).mean().sqrt()) / rms}
+        ok = ok and stack_err["max_err_over_rms"] <= 3e-2 and stack_err["rms_err_over_rms"] <= 1e-2
     return {"value": L * L / t, "unit": "cells/s", "cores": threads, "kind": "port",
             "sample": f"TMU pair (out+in, residuals) at L={L}, C=c={C}, fp32 torch on CPU, median of 3 after 1 "
                       f"warm-up, {t * 1e3:.1f} ms per pair",
-            "check": {"pair_max_err_over_rms": pair_err, "q8_rel_err_sample_rows": q8_err, "ok": ok}}
+            "check": {"pair_max_err_over_rms": pair_err, "q8_rel_err_sample_rows": q8_err,
+                      "block_stack_vs_oracle_fp16_stream": stack_err, "ok": ok}}
 
 
 def main():
@@ -284,10 +306,56 @@ def main():
                           "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK, "split_k": ws is not None}
         out["q8"] = qres
 
+    stack_case = None
+    if not args.no_stack:
+        # the transition kernel alone, in place on a copy of z
+        zs, blocks = W.block_stack(L, n_blocks=8, C=C, c=CL, H=4 * C, seed=0)
+        trunk = pkg.trunk.PairTrunk.from_weights(blocks, device=dev)
+        tr = trunk.blocks[0].transition
+        zt = zs.to(dev).contiguous()
+        for _ in range(5):
+            tr.run(zt, zt)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 50
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            tr.run(zt, zt)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        tfl = 4 * C * (4 * C) * L * L
+        out["transition"] = {"us": t * 1e6, "tflops": tfl / t / 1e12, "mfma_frac": tfl / t / MFMA_F16_PEAK,
+                             "gbs": 4 * C * L * L / t / 1e9}
+        # the block stack: one HIP graph of 8 blocks x 3 recycles (168 kernels), z reloaded per replay
+        recycles = 3
+        zbuf = torch.empty(1, L, L, C, dtype=torch.float16, device=dev)
+        z0s = zs.to(dev)
+        replay = trunk.graphed(zbuf, None, recycles=recycles)
+        zbuf.copy_(z0s)
+        replay()
+        torch.cuda.synchronize()
+        stack_out = zbuf.cpu()
+        ts = []
+        for _ in range(5):
+            zbuf.copy_(z0s)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e-3)
+        t = statistics.median(ts)
+        fl = 8 * recycles * (2 * sum(v["flops"] for v in counts.values()) + tfl)
+        out["block_stack"] = {"ms": t * 1e3, "blocks": 8, "recycles": recycles, "launch": "hip graph",
+                              "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
+                              "cells_per_s_per_block": L * L * 8 * recycles / t}
+        stack_case = (zs, blocks, stack_out)
+
     if args.copy_probe:
         copy_probe(dev)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(z, po, pi, pair_out, q8_samples)
+        out["cpu_baseline"] = cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case)
         out["speedup_vs_cpu"] = out["value"] / out["cpu_baseline"]["value"]
     print(json.dumps(out), flush=True)
     if not args.no_cpu and not out["cpu_baseline"]["check"]["ok"]:

@@ -7,17 +7,19 @@ Modules:
   kernels          -- one functional wrapper per C entry point (torch tensors in/out)
   trimul           -- TriMul / TriMulPair: the forward(pair_grid, visibility) module contract
   q8               -- Q8Linear: the quantized_matmul(transpose=True, group 64, bits 8) contract
-  var_hip_trimul   -- the reference-style variant plugin: apply(model)
+  trunk            -- PairTransition, TrunkBlock and PairTrunk (the FoldingTrunk drop-in)
+  var_hip_trimul   -- the reference-style variant plugin for the TMUs: apply(model)
+  var_hip_trunk    -- the variant plugin replacing the whole folding trunk: apply(model)
   workloads        -- seeded synthetic inputs of the benchmark configurations
 """
 
 from . import build, capi  # noqa: F401
 
-__all__ = ["build", "capi", "kernels", "trimul", "q8", "var_hip_trimul", "workloads"]
+__all__ = ["build", "capi", "kernels", "trimul", "q8", "trunk", "var_hip_trimul", "var_hip_trunk", "workloads"]
 
 
 def __getattr__(name):
-    if name in ("kernels", "trimul", "q8", "var_hip_trimul", "workloads"):
+    if name in ("kernels", "trimul", "q8", "trunk", "var_hip_trimul", "var_hip_trunk", "workloads"):
         import importlib
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)

@@ -27,6 +27,7 @@ SIGNATURES = {
                             _int, _int, _int, _vp]),
     "tmu_forward": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _int, _int, _int,
                            _int, _int, _int, _int, _vp]),
+    "pair_transition": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "q8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "q8_linear_ws": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
     "q8_linear_workspace_bytes": (_sz, [_int, _int, _int]),

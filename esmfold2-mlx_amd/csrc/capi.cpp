@@ -231,6 +231,27 @@ int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_
   return q8_linear_ws(x, q, s, b, nullptr, y, M, K, N, group, nullptr, 0, stream);
 }
 
+int pair_transition(const esm_half* z, esm_half* out, const float* ln_w, const float* ln_b, float eps,
+                    const esm_half* w1, const esm_half* w2, const esm_half* w3, int B, int L, int C, int hidden,
+                    void* stream) {
+  if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "pair_transition: B=%d L=%d must be >= 0", B, L);
+  if (C != 128) return fail(ESM_ERR_UNSUPPORTED, "pair_transition: C=%d (supported: 128)", C);
+  if (w2 ? hidden != 256 : (hidden != 256 && hidden != 512))
+    return fail(ESM_ERR_UNSUPPORTED, "pair_transition: H=%d (supported: ReLU 256 or 512, SwiGLU 256)", hidden);
+  if (B == 0 || L == 0) return ok();
+  if (L > kMaxL) return fail(ESM_ERR_SHAPE, "pair_transition: L=%d exceeds %d", L, kMaxL);
+  const size_t ncells = (size_t)B * L * L;
+  if (ncells * C * 2 >= (1ull << 31)) return fail(ESM_ERR_SHAPE, "pair_transition: B*L*L=%zu cells exceed 2 GB", ncells);
+  if (!z || !out || !ln_w || !ln_b || !w1 || !w3) return fail(ESM_ERR_NULL, "pair_transition: NULL pointer");
+  if (!aligned16(z) || !aligned16(out) || !aligned16(w1) || !aligned16(w3) || (w2 && !aligned16(w2)))
+    return fail(ESM_ERR_ALIGN, "pair_transition: z, out, w1, w2, w3 must be 16-byte aligned");
+  esm::TransitionArgs a{H(z), H(out), ln_w, ln_b, eps, H(w1), w2 ? H(w2) : nullptr, H(w3), ncells, 0, hidden};
+  const size_t ntiles = (ncells + 31) / 32;
+  a.ntiles = (int)ntiles;
+  const int grid = (int)(ntiles < (size_t)cu_count() ? ntiles : cu_count());
+  return hip_status(esm::launch_transition(a, grid, (hipStream_t)stream), "pair_transition launch");
+}
+
 size_t q8_packed_scales_bytes(int N, int K) {
   if (N <= 0 || K <= 0 || K % 64 != 0) return 0;
   return (size_t)((N + esm::kQ8TileN - 1) / esm::kQ8TileN) * (K / 64) * esm::kQ8TileN * sizeof(uint32_t);

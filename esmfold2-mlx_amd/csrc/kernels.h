@@ -68,6 +68,19 @@ constexpr int kQ8TileM = 64;
 constexpr int kQ8TileN = 160;
 constexpr int kQ8Waves = 4;
 
+struct TransitionArgs {
+  const half_t* z;      // [cells, C]
+  half_t* out;          // [cells, C], may be z
+  const float* ln_w;    // [C]
+  const float* ln_b;    // [C]
+  float eps;
+  const half_t* w1;     // [H, C]
+  const half_t* w2;     // [H, C] (SwiGLU) or nullptr (ReLU)
+  const half_t* w3;     // [C, H]
+  size_t ncells;
+  int ntiles, H;
+};
+
 // Cells per tile of the per-cell kernels (a) and (c).
 constexpr int kCellTile = 64;
 
@@ -76,6 +89,7 @@ hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s);
 hipError_t launch_contract(const ContractArgs& a, hipStream_t s);
 hipError_t launch_epilogue(const EpilogueArgs& a, int grid, hipStream_t s);
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s);
+hipError_t launch_transition(const TransitionArgs& a, int grid, hipStream_t s);
 hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st);
 hipError_t launch_q8_dequant(const uint8_t* q, const half_t* s, const half_t* b, half_t* w, int N, int K,
                              hipStream_t st);

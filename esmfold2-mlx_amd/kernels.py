@@ -88,6 +88,28 @@ def epilogue(x, z, mask, ln_in_w, ln_in_b, eps_in, ln_mix_w, ln_mix_b, eps_mix, 
     return out
 
 
+def transition(z, ln_w, ln_b, eps, w1, w3, w2=None, out=None):
+    """Kernel (e): z + W3 act(W1 LN(z)), act = ReLU (``w2`` None) or silu(W1 h) * (W2 h).
+    z [B, L, L, C] fp16; w1, w2 [H, C], w3 [C, H] fp16; ``out`` may be ``z`` (in place)."""
+    lib = capi.lib()
+    _dev(z, "z", F16)
+    B, L, L2, C = z.shape
+    if L2 != L:
+        raise capi.EsmError(-2, f"transition: z must be [B, L, L, C], got {tuple(z.shape)}")
+    H = w1.shape[0]
+    _dev(w1, "w1", F16)
+    _dev(w3, "w3", F16)
+    if w2 is not None:
+        _dev(w2, "w2", F16)
+    if tuple(w1.shape) != (H, C) or tuple(w3.shape) != (C, H) or (w2 is not None and tuple(w2.shape) != (H, C)):
+        raise capi.EsmError(-2, f"transition: w1 {tuple(w1.shape)}, w3 {tuple(w3.shape)} for C={C}")
+    out = torch.empty_like(z) if out is None else _dev(out, "out", F16)
+    capi.check(lib.pair_transition(z.data_ptr(), out.data_ptr(), _dev(ln_w, "ln_w", torch.float32).data_ptr(),
+                                   _dev(ln_b, "ln_b", torch.float32).data_ptr(), float(eps), w1.data_ptr(), _ptr(w2),
+                                   w3.data_ptr(), B, L, C, H, capi.stream_ptr()))
+    return out
+
+
 def q8_workspace_bytes(M: int, K: int, N: int) -> int:
     """Bytes of workspace q8_linear uses to split K at this shape (0: it runs unsplit)."""
     return int(capi.lib().q8_linear_workspace_bytes(M, K, N))

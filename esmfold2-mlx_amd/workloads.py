@@ -7,6 +7,9 @@ seeded draws; both sides of a comparison see identical bytes.
   incoming update's weights: proj_bundle.weight [4c, C], proj_gate.weight [C, C],
   proj_emit.weight [C, c], in that order, each N(0, 1/fan_in); LayerNorm gamma = 1,
   beta = 0 (no draws). fp32 master weights; z cast to ``dtype`` after the fp32 draw.
+* ``block_stack``: the pair-trunk block stack: z ~ N(0, 1), then per block the
+  outgoing and the incoming update's weights (as above) and the transition's:
+  W1 [H, C] ~ N(0, 1/C), W3 [C, H] ~ N(0, 1/H) (ReLU MLP, no biases, LN gamma 1 beta 0).
 * ``q8_inputs``: x [M, K] fp16 ~ N(0, 1); codes q [N, K] ~ U{0..255}; scales
   s [N, K/64] ~ U(0.001, 0.01) and biases b ~ N(0, 0.1), fp16; drawn in that order.
 """
@@ -61,6 +64,35 @@ def pair_inputs(L: int, C: int = 128, c: int = 128, seed: int = 0, dtype=torch.f
         v = (torch.arange(L) < pad_from).to(torch.float32)
         mask = (v[:, None] * v[None, :]).expand(B, L, L).contiguous()
     return z, mask, p_out, p_in
+
+
+@dataclass
+class TransitionParams:
+    """The pair transition's weights: w1 [H, C], w3 [C, H], w2 [H, C] for SwiGLU (None: ReLU)."""
+
+    ln_w: torch.Tensor
+    ln_b: torch.Tensor
+    w1: torch.Tensor
+    w3: torch.Tensor
+    w2: torch.Tensor | None = None
+    eps: float = EPS
+
+
+def transition_params(gen: torch.Generator, C: int, H: int) -> TransitionParams:
+    f32 = torch.float32
+    w1 = torch.randn(H, C, generator=gen, dtype=f32) * (1.0 / C) ** 0.5
+    w3 = torch.randn(C, H, generator=gen, dtype=f32) * (1.0 / H) ** 0.5
+    return TransitionParams(torch.ones(C, dtype=f32), torch.zeros(C, dtype=f32), w1, w3)
+
+
+def block_stack(L: int, n_blocks: int = 8, C: int = 128, c: int = 128, H: int = 512, seed: int = 0,
+                dtype=torch.float16, B: int = 1):
+    """(z, [(T_out params, T_in params, transition params)] per block)."""
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn(B, L, L, C, generator=g, dtype=torch.float32).to(dtype)
+    blocks = [(tmu_params(g, C, c, True), tmu_params(g, C, c, False), transition_params(g, C, H))
+              for _ in range(n_blocks)]
+    return z, blocks
 
 
 def q8_inputs(M: int, K: int, N: int, seed: int = 0, group: int = 64):

@@ -143,6 +143,23 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
                 int c, int outgoing, int residual, int out_mask, void* stream);
 
 /*
+ * Kernel (e): the pair transition, out = z + W3 act(W1 LN(z)) on every cell, with
+ * act = ReLU (w2 == NULL: transformers' EsmFoldResidueMLP without biases, the
+ * block-stack workload's 128 -> H -> 128 MLP) or SwiGLU, act = silu(W1 h) * (W2 h)
+ * (the reference's transition: fast_trunk.py:35-42 with w1 = ffn.w12.weight[:H],
+ * w2 = ffn.w12.weight[H:], w3 = ffn.w3.weight; mlx_trunk.py:96-99 and its addmm
+ * residual, mlx_trunk_kernels.py:236-239). No biases (fast_trunk.py:59).
+ *
+ * z, out [B, L, L, C] fp16 cell-major (out may be z); ln_w, ln_b [C] fp32;
+ * w1, w2 [H, C] fp16; w3 [C, H] fp16 (torch [out, in] layouts). fp32 statistics and
+ * accumulation; the hidden activations and the output are each rounded once to fp16.
+ * Supported: C = 128; ReLU H = 256 or 512; SwiGLU H = 256.
+ */
+int pair_transition(const esm_half* z, esm_half* out, const float* ln_w, const float* ln_b, float eps,
+                    const esm_half* w1, const esm_half* w2, const esm_half* w3, int B, int L, int C, int H,
+                    void* stream);
+
+/*
  * Kernel (d): MLX-affine 8-bit weight-only linear, y = x . W^T with
  * W[n, k] = RN_fp16(s[n, k/64] * q[n, k] + b[n, k/64]) (dequantised in registers,
  * one fp16 FMA rounding) and fp32 accumulation; y rounded once to fp16.

@@ -75,16 +75,21 @@ def draw_blocks(gen: torch.Generator, n_blocks: int, C: int, c: int, H: int):
             for _ in range(n_blocks)]
 
 
-def block_forward(z, mask, blk: BlockWeights):
-    """mlx_trunk.py:93-99 order: z += T_out(z); z += T_in(z); z = transition(z)."""
-    z = z + trimul(z, mask, blk.tri_out, True)
-    z = z + trimul(z, mask, blk.tri_in, False)
-    return transition(z, blk.trans)
+def block_forward(z, mask, blk: BlockWeights, store=None):
+    """mlx_trunk.py:93-99 order: z += T_out(z); z += T_in(z); z = transition(z).
+
+    ``store`` (e.g. torch.float16) rounds the residual stream to that dtype after every
+    residual add, as the reference's fp16 trunk stores every intermediate, the residual
+    stream included, in fp16 (mlx_trunk.py:8-19); None keeps the working precision."""
+    r = (lambda t: t) if store is None else (lambda t: t.to(store).to(t.dtype))  # noqa: E731
+    z = r(z + trimul(z, mask, blk.tri_out, True))
+    z = r(z + trimul(z, mask, blk.tri_in, False))
+    return r(transition(z, blk.trans))
 
 
-def stack_forward(z, mask, blocks, recycles: int = 1):
+def stack_forward(z, mask, blocks, recycles: int = 1, store=None):
     """The block stack applied ``recycles`` times with z carried between passes."""
     for _ in range(recycles):
         for blk in blocks:
-            z = block_forward(z, mask, blk)
+            z = block_forward(z, mask, blk, store)
     return z

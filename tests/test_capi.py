@@ -25,7 +25,8 @@ def lib(pkg):
 def test_header_declares_the_entry_points():
     names = declared_functions()
     for n in ("tmu_project", "tmu_contract", "tmu_epilogue", "tmu_forward", "q8_linear", "q8_linear_ws",
-              "q8_linear_workspace_bytes", "q8_pack_scales", "q8_packed_scales_bytes", "q8_dequant", "esm_last_error", "esm_version", "tmu_workspace_bytes", "tmu_leading_dim"):
+              "q8_linear_workspace_bytes", "q8_pack_scales", "q8_packed_scales_bytes",
+              "pair_transition", "q8_dequant", "esm_last_error", "esm_version", "tmu_workspace_bytes", "tmu_leading_dim"):
         assert n in names
 
 
@@ -66,6 +67,11 @@ def test_rejects_null_and_bad_shapes(lib):
     assert lib.q8_linear(None, None, None, None, None, 4, 128, 64, 32, None) == -4  # group 32
     assert lib.q8_dequant(None, None, None, None, 64, 64, 64, None) == -1
     assert lib.q8_linear_ws(None, None, None, None, None, None, 5, 1024, 64, 64, None, 0, None) == -1
+    assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 1, 8, 128, 512, None) == -1
+    assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 1, 8, 256, 512, None) == -4
+    assert lib.pair_transition(None, None, None, None, 1e-5, None, ctypes.c_void_p(4096), None, 1, 8, 128, 512,
+                               None) == -4  # SwiGLU at H=512
+    assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 0, 8, 128, 512, None) == 0
     assert lib.q8_pack_scales(None, None, None, 64, 128, 64, None) == -1
     assert lib.q8_pack_scales(None, None, None, 64, 100, 64, None) == -2
     assert lib.q8_packed_scales_bytes(64, 128) == 1 * 2 * 160 * 4 and lib.q8_packed_scales_bytes(161, 64) == 2 * 160 * 4

@@ -1,0 +1,154 @@
+"""GPU tests of the block stack, the FoldingTrunk drop-in and the two variant plugins.
+
+The stack is compared with the oracle's stack in fp64 with fp32 master weights, with
+its residual stream stored in fp16 after every residual add as the reference's fp16
+trunk stores it (mlx_trunk.py:8-19), and with an fp64 stream.
+
+Bars, on the accumulated update u = z_out - z_in: for one block (three ops), the
+triangle update's max|err| <= 1e-2 x RMS(u). Deeper stacks accumulate one op's error per
+residual add (each op sits near 3e-3 x RMS of its own update) and fp16 roundings of a
+growing z, where a single-ulp difference of the largest values (|z| up to 16 x RMS(u))
+already reaches 1e-2 x RMS(u): measured on the GPU at L=40, max|err| / RMS(u) is 5e-3
+after 1 block, 9e-3 after 8 and 1.4e-2 to 1.7e-2 after 8 blocks x 3 recycles, while the
+normwise error stays near 2e-3. For those the bar is normwise RMS(err) <= 1e-2 x RMS(u)
+plus max|err| <= 3e-2 x RMS(u).
+"""
+
+import pytest
+import torch
+
+from oracle import tmu as otmu, transition as otr
+from tests import ref_modules
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+FIELDS = ("w_bundle", "w_emit", "w_gate", "ln_in_w", "ln_in_b", "ln_mix_w", "ln_mix_b", "ln_in_eps", "ln_mix_eps",
+          "outgoing")
+
+
+def _oracle_blocks(blocks, dtype=torch.float64):
+    out = []
+    for po, pi, pt in blocks:
+        o = otmu.TriMulWeights(**{f: getattr(po, f) for f in FIELDS}).to(dtype)
+        i = otmu.TriMulWeights(**{f: getattr(pi, f) for f in FIELDS}).to(dtype)
+        t = otr.TransitionWeights(pt.ln_w.to(dtype), pt.ln_b.to(dtype), pt.w1.to(dtype), pt.w3.to(dtype),
+                                  None if pt.w2 is None else pt.w2.to(dtype), eps=pt.eps)
+        out.append(otr.BlockWeights(o, i, t))
+    return out
+
+
+def _check(got, z0, ref, bar=1e-2, norm_bar=None):
+    upd_ref = ref - z0.double()
+    d = got.double().cpu() - ref
+    err = float(d.abs().max())
+    rms = float(upd_ref.pow(2).mean().sqrt())
+    assert err <= bar * rms, f"max|err| {err:.3e} vs RMS(update) {rms:.3e}"
+    if norm_bar is not None:
+        nrm = float(d.pow(2).mean().sqrt())
+        assert nrm <= norm_bar * rms, f"RMS(err) {nrm:.3e} vs RMS(update) {rms:.3e}"
+    return err / rms
+
+
+@pytest.mark.parametrize("L,n_blocks,recycles,pad", [(40, 8, 3, None), (64, 2, 1, 50), (33, 1, 2, None),
+                                                     (50, 1, 1, 41)])
+def test_stack_matches_oracle(gpu_lib, pkg, L, n_blocks, recycles, pad):
+    z, blocks = pkg.workloads.block_stack(L, n_blocks=n_blocks, seed=L)
+    mask = None
+    if pad is not None:
+        v = (torch.arange(L) < pad).float()
+        mask = (v[:, None] * v[None, :])[None].contiguous()
+    trunk = pkg.trunk.PairTrunk.from_weights(blocks)
+    z16 = z.to(DEV).contiguous()
+    trunk.run_(z16, None if mask is None else mask.to(DEV).half(), recycles)
+    m64 = None if mask is None else mask.double()
+    bars = {} if n_blocks * recycles <= 1 else {"bar": 3e-2, "norm_bar": 1e-2}
+    ref16 = otr.stack_forward(z.double(), m64, _oracle_blocks(blocks), recycles, store=torch.float16)
+    r16 = _check(z16.cpu(), z, ref16, **bars)
+    ref = otr.stack_forward(z.double(), m64, _oracle_blocks(blocks), recycles)
+    r64 = _check(z16.cpu(), z, ref, **bars)
+    print(f"stack L={L} {n_blocks}x{recycles}: err/RMS {r16:.2e} (fp16 stream), {r64:.2e} (fp64 stream)")
+
+
+def test_folding_trunk_drop_in_contract(gpu_lib, pkg):
+    z, blocks = pkg.workloads.block_stack(24, n_blocks=2, seed=3)
+    trunk = pkg.trunk.PairTrunk.from_weights(blocks)
+    trunk.set_chunk_size(64)          # accepted, ignored
+    trunk.set_kernel_backend("any")   # accepted, ignored
+    pair = z.to(DEV).float()
+    keep = pair.clone()
+    out = trunk(pair)
+    assert out.dtype == torch.float32 and out.device == pair.device and out.shape == pair.shape
+    assert torch.equal(pair, keep), "the trunk wrote into its input"
+    ones = torch.ones(1, 24, 24, device=DEV)
+    assert torch.equal(trunk(pair, ones), out), "an all-ones mask must be elided"
+    ref = otr.stack_forward(z.double(), None, _oracle_blocks(blocks), 1, store=torch.float16)
+    _check(out, z, ref, bar=3e-2, norm_bar=1e-2)
+
+
+def test_var_hip_trunk_plugin_swiglu(gpu_lib, pkg):
+    # the reference's trunk layout (SwiGLU transitions, wrapped TMUs) through apply(model)
+    z, blocks = pkg.workloads.block_stack(20, n_blocks=2, H=256, seed=4)
+    g = torch.Generator().manual_seed(9)
+    for _, _, pt in blocks:
+        pt.w2 = torch.randn(256, 128, generator=g) * 128 ** -0.5
+    model = ref_modules.Model(blocks)
+    pkg.var_hip_trunk.apply(model)
+    assert isinstance(model.folding_trunk, pkg.trunk.PairTrunk)
+    out = model.folding_trunk(z.to(DEV).float())
+    ref = otr.stack_forward(z.double(), None, _oracle_blocks(blocks), 1, store=torch.float16)
+    _check(out, z, ref, bar=3e-2, norm_bar=1e-2)
+
+
+def test_var_hip_trimul_plugin(gpu_lib, pkg):
+    z, mask, po, pi = pkg.workloads.pair_inputs(30, seed=2, pad_from=25)
+    _, blocks = pkg.workloads.block_stack(4, n_blocks=1, H=256)
+    pt = blocks[0][2]
+    pt.w2 = torch.randn(256, 128, generator=torch.Generator().manual_seed(1)) * 128 ** -0.5  # SwiGLU, as the reference
+    model = ref_modules.Model([(po, pi, pt)])
+    assert pkg.var_hip_trimul.apply(model) == 2
+    blk = model.folding_trunk.blocks[0]
+    zd, md = z.to(DEV), mask.to(DEV)
+    for wrapped, p, outgoing in ((blk.tri_mul_out, po, True), (blk.tri_mul_in, pi, False)):
+        upd = wrapped._engine(zd, md)  # the patched per-module forward: the update only
+        ref = otmu.trimul(z.double(), mask.double(), otmu.TriMulWeights(**{f: getattr(p, f) for f in FIELDS})
+                          .to(torch.float64), outgoing)
+        err = float((upd.double().cpu() - ref).abs().max())
+        assert err <= 1e-2 * float(ref.pow(2).mean().sqrt())
+        assert torch.equal(wrapped._engine(zd), wrapped._engine(zd, torch.ones_like(md)))  # None == all ones
+    with pytest.raises(ValueError):
+        pkg.var_hip_trimul.apply(torch.nn.Linear(2, 2))
+
+
+def test_graph_replay_matches_eager(gpu_lib, pkg):
+    z, blocks = pkg.workloads.block_stack(48, n_blocks=2, seed=6)
+    trunk = pkg.trunk.PairTrunk.from_weights(blocks)
+    eager = z.to(DEV).contiguous()
+    trunk.run_(eager, None, 2)
+    buf = torch.empty_like(eager)
+    replay = trunk.graphed(buf, None, recycles=2)
+    for _ in range(3):  # several replays, with eager work and synchronisations between them
+        buf.copy_(z.to(DEV))
+        torch.cuda.synchronize()
+        replay()
+        torch.cuda.synchronize()
+        assert torch.equal(buf.view(torch.int16), eager.view(torch.int16))
+        _ = (eager.float() * 2).sum().item()
+
+
+def test_residue_mlp_transition_matches_transformers(gpu_lib, pkg):
+    tf = pytest.importorskip("transformers.models.esm.modeling_esmfold")
+    mlp = tf.EsmFoldResidueMLP(128, 512).eval()
+    with torch.no_grad():
+        for lin in (mlp.mlp[1], mlp.mlp[3]):
+            lin.bias.zero_()
+    tr = pkg.trunk.PairTransition.from_residue_mlp(mlp)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 17, 17, 128, generator=g).half()
+    got = tr(x.to(DEV)).double().cpu()
+    with torch.no_grad():
+        m64 = mlp.double()
+        for lin in (m64.mlp[1], m64.mlp[3]):
+            lin.weight.copy_(lin.weight.half().double())  # the kernel's fp16 weights
+        ref = m64(x.double())
+    upd = ref - x.double()
+    assert float((got - ref).abs().max()) <= 1e-2 * float(upd.pow(2).mean().sqrt())

@@ -56,3 +56,26 @@ def test_block_order():
     z1b = z + tmu.trimul(z, None, blk.tri_in, False)
     z2b = z1b + tmu.trimul(z1b, None, blk.tri_out, True)
     assert not torch.allclose(z2, z2b)
+
+
+def test_stack_store_and_recycles():
+    g = torch.Generator().manual_seed(3)
+    blocks = [tr.BlockWeights(b.tri_out.to(D), b.tri_in.to(D),
+                              tr.TransitionWeights(b.trans.ln_w.double(), b.trans.ln_b.double(), b.trans.w1.double(),
+                                                   b.trans.w3.double()))
+              for b in tr.draw_blocks(g, 2, 8, 8, 32)]
+    z = torch.randn(1, 4, 4, 8, generator=g, dtype=D)
+    # storing at the working precision is the identity
+    torch.testing.assert_close(tr.stack_forward(z, None, blocks, 2, store=D), tr.stack_forward(z, None, blocks, 2),
+                               rtol=0, atol=0)
+    # recycles compose: two passes = one pass applied to one pass's output
+    once = tr.stack_forward(z, None, blocks, 1)
+    torch.testing.assert_close(tr.stack_forward(z, None, blocks, 2), tr.stack_forward(once, None, blocks, 1),
+                               rtol=0, atol=0)
+    # an fp16 residual stream leaves every stored value representable in fp16, and stays
+    # within fp16 rounding of the fp64 stream
+    z16 = tr.stack_forward(z.half().double(), None, blocks, 1, store=torch.float16)
+    assert torch.equal(z16, z16.half().double())
+    ref = tr.stack_forward(z.half().double(), None, blocks, 1)
+    assert float((z16 - ref).abs().max()) <= 0.05 * float(ref.abs().max())
+    assert not torch.equal(z16, ref)

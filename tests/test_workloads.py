@@ -25,3 +25,19 @@ def test_q8_inputs_match_the_oracle(pkg):
     ref = q8.make_q8_inputs(5, 256, 64, seed=11)
     for a, b in zip(got, ref):
         assert np.array_equal(a.numpy(), b)
+
+
+def test_block_stack_matches_the_oracle(pkg):
+    from oracle import transition as otr
+    z, blocks = pkg.workloads.block_stack(9, n_blocks=3, H=256, seed=5)
+    g = torch.Generator().manual_seed(5)
+    z2 = torch.randn(1, 9, 9, 128, generator=g).half()
+    ref = otr.draw_blocks(g, 3, 128, 128, 256)
+    assert torch.equal(z, z2)
+    for (po, pi, pt), rb in zip(blocks, ref):
+        for a, b in ((po, rb.tri_out), (pi, rb.tri_in)):
+            for f in ("w_bundle", "w_emit", "w_gate"):
+                assert torch.equal(getattr(a, f), getattr(b, f))
+        for f in ("ln_w", "ln_b", "w1", "w3"):
+            assert torch.equal(getattr(pt, f), getattr(rb.trans, f))
+        assert pt.w2 is None and rb.trans.w2 is None
