@@ -15,6 +15,9 @@ Also reported on the same JSON line:
                 at L=238 (time, TFLOP/s, fraction of MFMA peak);
   block_stack   the pair-trunk block stack at L=238: 8 blocks of (T_out, T_in,
                 transition) x 3 recycles with z carried, replayed as one HIP graph;
+  esmc_block    one ESMC transformer block at 238 tokens, D=2560, 40 heads, FFN 5120
+                (its wqkv, wo, w1, w2 8-bit linears and the LN / RoPE / attention /
+                SwiGLU kernels), eager launches;
   cpu_baseline  the CPU oracle (torch fp32 restatement of the reference's
                 _trimul_forward) on the host cores, a bounded sample of the same
                 workload (rank 0, N=1 only). This leg is also the checker: the
@@ -77,6 +80,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-q8", action="store_true", help="skip the q8 linear figures")
     ap.add_argument("--no-stack", action="store_true", help="skip the transition and block-stack figures")
+    ap.add_argument("--no-esmc", action="store_true", help="skip the ESMC block figure")
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 64 MiB device copy 10 times (counter calibration under rocprofv3)")
@@ -94,7 +98,7 @@ def copy_probe(dev, reps: int = 10, nbytes: int = 64 << 20):
     torch.cuda.synchronize()
 
 
-def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None):
+def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=None):
     """The CPU oracle in fp32 on the host cores: 1 warm-up, median of 3 TMU pairs at L=238.
     Also the checker of the GPU leg: the benchmarked pair output against the oracle's
     (max|err| / RMS(update), bar 1e-2) and the sampled q8 rows (normwise, bar 1e-3)."""
@@ -138,11 +142,25 @@ def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None):
         rms = float(u.pow(2).mean().sqrt())
         stack_err = {"max_err_over_rms": float(d.abs().max()) / rms, "rms_err_over_rms": float(d.pow(2).mean().sqrt()) / rms}
         ok = ok and stack_err["max_err_over_rms"] <= 3e-2 and stack_err["rms_err_over_rms"] <= 1e-2
+    esmc_err = None
+    if esmc_case is not None:
+        # the ESMC block against the oracle (fp32 on the CPU, fp16-rounded dequantised weights)
+        from oracle import esmc as oe
+        xe, ln, lin, rs, heads, got = esmc_case
+        qw = {n: oe.Q8Weights(*(t.numpy() for t in lin[n])) for n in lin}
+        pw = oe.EsmcBlockWeights(ln["ln1_w"], ln["ln1_b"], ln["q_ln"], ln["k_ln"], ln["ln2_w"], ln["ln2_b"],
+                                 qw["wqkv"], qw["wo"], qw["w1"], qw["w2"])
+        with torch.no_grad():
+            ref = oe.block_forward(pw, xe.double(), None, n_heads=heads, res_scale=rs, weights="f16")
+        u = ref - xe.double()
+        esmc_err = float((got.double() - ref).abs().max()) / float(u.pow(2).mean().sqrt())
+        ok = ok and esmc_err <= 1e-2
     return {"value": L * L / t, "unit": "cells/s", "cores": threads, "kind": "port",
             "sample": f"TMU pair (out+in, residuals) at L={L}, C=c={C}, fp32 torch on CPU, median of 3 after 1 "
                       f"warm-up, {t * 1e3:.1f} ms per pair",
             "check": {"pair_max_err_over_rms": pair_err, "q8_rel_err_sample_rows": q8_err,
-                      "block_stack_vs_oracle_fp16_stream": stack_err, "ok": ok}}
+                      "block_stack_vs_oracle_fp16_stream": stack_err, "esmc_block_max_err_over_rms": esmc_err,
+                      "ok": ok}}
 
 
 def main():
@@ -352,10 +370,36 @@ def main():
                               "cells_per_s_per_block": L * L * 8 * recycles / t}
         stack_case = (zs, blocks, stack_out)
 
+    esmc_case = None
+    if not args.no_esmc:
+        ED, EF, EH = 2560, 5120, 40
+        xe, ln, lin = W.esmc_block_inputs(L, ED, EF, seed=0)
+        blk = pkg.esmc.EsmcBlock.from_arrays(ln, lin, EH, device=dev)
+        rs = (80 / 36) ** 0.5
+        xed = xe.to(dev)
+        for _ in range(3):
+            ye = blk(xed, None, res_scale=rs)
+        torch.cuda.synchronize()
+        esmc_out = ye.cpu()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        e0.record(stream)
+        for _ in range(reps):
+            blk(xed, None, res_scale=rs)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        fl = 2 * L * ED * (3 * ED + ED + 2 * EF + EF) + 4 * L * L * ED  # linears + attention
+        wbytes = sum(q.numel() + 4 * s_.numel() for q, s_, _ in lin.values())
+        out["esmc_block"] = {"us": t * 1e6, "tokens": L, "D": ED, "ffn": EF, "heads": EH, "launch": "eager",
+                             "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
+                             "weight_gbs": wbytes / t / 1e9, "weight_hbm_frac": wbytes / t / HBM_PEAK}
+        esmc_case = (xe, ln, lin, rs, EH, esmc_out)
+
     if args.copy_probe:
         copy_probe(dev)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case)
+        out["cpu_baseline"] = cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case, esmc_case)
         out["speedup_vs_cpu"] = out["value"] / out["cpu_baseline"]["value"]
     print(json.dumps(out), flush=True)
     if not args.no_cpu and not out["cpu_baseline"]["check"]["ok"]:

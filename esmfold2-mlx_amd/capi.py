@@ -28,6 +28,10 @@ SIGNATURES = {
     "tmu_forward": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _int, _int, _int,
                            _int, _int, _int, _int, _vp]),
     "pair_transition": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
+    "esmc_layer_norm": (_int, [_vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int, _int, _vp]),
+    "esmc_qk_rope": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _f32, _vp]),
+    "esmc_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _f32, _vp]),
+    "esmc_swiglu": (_int, [_vp, _vp, _int, _int, _vp]),
     "q8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "q8_linear_ws": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
     "q8_linear_workspace_bytes": (_sz, [_int, _int, _int]),

@@ -3,6 +3,7 @@
 // memory; every launch goes on the caller's stream.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -250,6 +251,55 @@ int pair_transition(const esm_half* z, esm_half* out, const float* ln_w, const f
   a.ntiles = (int)ntiles;
   const int grid = (int)(ntiles < (size_t)cu_count() ? ntiles : cu_count());
   return hip_status(esm::launch_transition(a, grid, (hipStream_t)stream), "pair_transition launch");
+}
+
+int esmc_layer_norm(const float* x, const esm_half* y, float alpha, float* x_out, const float* w, const float* b,
+                    float eps, esm_half* h, float* h_fp32, int M, int D, void* stream) {
+  if (M < 0 || D <= 0) return fail(ESM_ERR_SHAPE, "esmc_layer_norm: M=%d D=%d", M, D);
+  if (D % 8 != 0 || D > 8192) return fail(ESM_ERR_UNSUPPORTED, "esmc_layer_norm: D=%d (multiple of 8, <= 8192)", D);
+  if (M == 0) return ok();
+  if (!x || !w || (!h == !h_fp32) || (y && !x_out))
+    return fail(ESM_ERR_NULL, "esmc_layer_norm: NULL pointer (exactly one of h, h_fp32 is written)");
+  if (!aligned16(x) || (h && !aligned16(h)) || (h_fp32 && !aligned16(h_fp32)) ||
+      (y && (!aligned16(y) || !aligned16(x_out))))
+    return fail(ESM_ERR_ALIGN, "esmc_layer_norm: x, y, x_out, h, h_fp32 must be 16-byte aligned");
+  esm::EsmcLnArgs a{x, y ? H(y) : nullptr, alpha, x_out, w, b, eps, h ? H(h) : nullptr, h_fp32, M, D};
+  return hip_status(esm::launch_esmc_ln(a, (hipStream_t)stream), "esmc_layer_norm launch");
+}
+
+int esmc_qk_rope(const esm_half* qkv, const float* q_ln, const float* k_ln, float eps, esm_half* q, esm_half* k,
+                 esm_half* v, int B, int L, int n_heads, int head_dim, float rope_base, void* stream) {
+  if (B < 0 || L < 0 || n_heads <= 0) return fail(ESM_ERR_SHAPE, "esmc_qk_rope: B=%d L=%d heads=%d", B, L, n_heads);
+  if (head_dim != 64 || n_heads * 64 > 4096)
+    return fail(ESM_ERR_UNSUPPORTED, "esmc_qk_rope: head_dim=%d heads=%d (head_dim 64, width <= 4096)", head_dim,
+                n_heads);
+  if (B == 0 || L == 0) return ok();
+  if (!qkv || !q_ln || !k_ln || !q || !k || !v) return fail(ESM_ERR_NULL, "esmc_qk_rope: NULL pointer");
+  if (!aligned16(qkv) || !aligned16(v)) return fail(ESM_ERR_ALIGN, "esmc_qk_rope: qkv, v must be 16-byte aligned");
+  esm::EsmcRopeArgs a{H(qkv), q_ln, k_ln, eps, H(q), H(k), H(v), B, L, n_heads, std::log2(rope_base)};
+  return hip_status(esm::launch_esmc_qk_rope(a, (hipStream_t)stream), "esmc_qk_rope launch");
+}
+
+int esmc_attention(const esm_half* q, const esm_half* k, const esm_half* v, const int* sequence_id, esm_half* o, int B,
+                   int L, int n_heads, int head_dim, float scale, void* stream) {
+  if (B < 0 || L < 0 || n_heads <= 0) return fail(ESM_ERR_SHAPE, "esmc_attention: B=%d L=%d heads=%d", B, L, n_heads);
+  if (head_dim != 64 || L > 512) return fail(ESM_ERR_UNSUPPORTED, "esmc_attention: head_dim=%d L=%d (64, <= 512)",
+                                             head_dim, L);
+  if (B == 0 || L == 0) return ok();
+  if ((long long)B * n_heads > 65535) return fail(ESM_ERR_SHAPE, "esmc_attention: B*heads=%d too large", B * n_heads);
+  if (!q || !k || !v || !o) return fail(ESM_ERR_NULL, "esmc_attention: NULL pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(o) & 7u))
+    return fail(ESM_ERR_ALIGN, "esmc_attention: q, k, v must be 16-byte and o 8-byte aligned");
+  esm::EsmcAttnArgs a{H(q), H(k), H(v), sequence_id, H(o), B, L, n_heads, scale * 1.4426950408889634f};
+  return hip_status(esm::launch_esmc_attention(a, (hipStream_t)stream), "esmc_attention launch");
+}
+
+int esmc_swiglu(const esm_half* x12, esm_half* y, int M, int F, void* stream) {
+  if (M < 0 || F <= 0 || F % 8 != 0) return fail(ESM_ERR_SHAPE, "esmc_swiglu: M=%d F=%d (F multiple of 8)", M, F);
+  if (M == 0) return ok();
+  if (!x12 || !y) return fail(ESM_ERR_NULL, "esmc_swiglu: NULL pointer");
+  if (!aligned16(x12) || !aligned16(y)) return fail(ESM_ERR_ALIGN, "esmc_swiglu: x12, y must be 16-byte aligned");
+  return hip_status(esm::launch_esmc_swiglu(H(x12), H(y), (size_t)M, F, (hipStream_t)stream), "esmc_swiglu launch");
 }
 
 size_t q8_packed_scales_bytes(int N, int K) {

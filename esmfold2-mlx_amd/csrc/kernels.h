@@ -81,6 +81,41 @@ struct TransitionArgs {
   int ntiles, H;
 };
 
+struct EsmcLnArgs {
+  const float* x;       // [M, D] fp32 residual
+  const half_t* y;      // [M, D] or nullptr: x_out = x + alpha * y
+  float alpha;
+  float* x_out;         // [M, D] (may be x; unused without y)
+  const float* w;       // [D]
+  const float* b;       // [D] or nullptr
+  float eps;
+  half_t* h;            // [M, D] LN output (fp16), or nullptr
+  float* h32;           // [M, D] LN output (fp32), or nullptr
+  int M, D;
+};
+
+struct EsmcRopeArgs {
+  const half_t* qkv;    // [B*L, 3D]
+  const float* q_ln;    // [D]
+  const float* k_ln;    // [D]
+  float eps;
+  half_t* q;            // [B, H, L, 64]
+  half_t* k;
+  half_t* v;
+  int B, L, H;
+  float log2_base;
+};
+
+struct EsmcAttnArgs {
+  const half_t* q;      // [B, H, L, 64]
+  const half_t* k;
+  const half_t* v;
+  const int* sid;       // [B, L] chain ids or nullptr
+  half_t* o;            // [B, L, H*64]
+  int B, L, H;
+  float scale_log2;     // scale * log2(e)
+};
+
 // Cells per tile of the per-cell kernels (a) and (c).
 constexpr int kCellTile = 64;
 
@@ -90,6 +125,10 @@ hipError_t launch_contract(const ContractArgs& a, hipStream_t s);
 hipError_t launch_epilogue(const EpilogueArgs& a, int grid, hipStream_t s);
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s);
 hipError_t launch_transition(const TransitionArgs& a, int grid, hipStream_t s);
+hipError_t launch_esmc_ln(const EsmcLnArgs& a, hipStream_t s);
+hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s);
+hipError_t launch_esmc_attention(const EsmcAttnArgs& a, hipStream_t s);
+hipError_t launch_esmc_swiglu(const half_t* x12, half_t* y, size_t M, int F, hipStream_t s);
 hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st);
 hipError_t launch_q8_dequant(const uint8_t* q, const half_t* s, const half_t* b, half_t* w, int N, int K,
                              hipStream_t st);

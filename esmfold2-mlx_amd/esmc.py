@@ -1,0 +1,181 @@
+"""The ESMC language model's transformer blocks on the HIP path: the drop-in for
+``model.esmc`` that the reference's MLXEsmc is (mlx_esmc.py:105-200).
+
+Each block is upstream's EsmcUnifiedTransformerBlock as mlx_esmc.py:84-102 restates it:
+pre-LN attention with QK-LayerNorm over all heads (weights only) and NeoX RoPE, then
+pre-LN SwiGLU, both residual adds divided by sqrt(n_layers / 36). The four linears are
+8-bit (``Q8Linear``: group 64, fp16 scales and biases, fp32 accumulation); every other
+op is a gfx950 kernel of the C ABI (``esmc_*``). The residual stream is fp32
+(the reference's default, ``residual=mx.float32``) and lives in the hidden-states slab
+the fold reads: block i reads hidden_states[i] and its second residual add writes
+hidden_states[i + 1], fused with the next block's input LayerNorm (or the final norm).
+"""
+
+from __future__ import annotations
+
+import math
+from types import SimpleNamespace
+
+import torch
+from torch import nn
+
+from . import kernels
+from .q8 import Q8Linear
+
+EPS = 1e-5
+LINEARS = ("wqkv", "wo", "w1", "w2")
+
+
+class EsmcBlock(nn.Module):
+    def __init__(self, ln1_w, ln1_b, q_ln, k_ln, ln2_w, ln2_b, wqkv: Q8Linear, wo: Q8Linear, w1: Q8Linear,
+                 w2: Q8Linear, n_heads: int, device=None):
+        super().__init__()
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        f = lambda t: t.detach().to(device=dev, dtype=torch.float32).contiguous()  # noqa: E731
+        for n, t in (("ln1_w", ln1_w), ("ln1_b", ln1_b), ("q_ln", q_ln), ("k_ln", k_ln), ("ln2_w", ln2_w),
+                     ("ln2_b", ln2_b)):
+            self.register_buffer(n, f(t))
+        self.wqkv, self.wo, self.w1, self.w2 = wqkv, wo, w1, w2
+        self.D = wo.out_features
+        self.F = w2.in_features
+        self.n_heads = n_heads
+        if self.D != n_heads * 64 or wqkv.out_features != 3 * self.D or w1.out_features != 2 * self.F:
+            raise ValueError(f"ESMC block shapes: D={self.D}, heads={n_heads}, wqkv {wqkv.out_features}, "
+                             f"w1 {w1.out_features}, w2 in {self.F}")
+
+    @classmethod
+    def from_params(cls, p: dict, n_heads: int = 40, device=None) -> "EsmcBlock":
+        """From one layer's arrays under the reference's names (mlx_esmc.py:53-75): ln1_w, ln1_b,
+        q_ln, k_ln, ln2_w, ln2_b, and per linear `name` (uint32 codes [N, K/4], four per word,
+        little-endian), `name_s`, `name_b` (fp16 [N, K/64])."""
+        t = lambda a: a if isinstance(a, torch.Tensor) else torch.as_tensor(a)  # noqa: E731
+        lin = {n: Q8Linear.from_packed_u32(t(p[n]), t(p[n + "_s"]), t(p[n + "_b"]), device=device) for n in LINEARS}
+        return cls(t(p["ln1_w"]), t(p["ln1_b"]), t(p["q_ln"]), t(p["k_ln"]), t(p["ln2_w"]), t(p["ln2_b"]),
+                   lin["wqkv"], lin["wo"], lin["w1"], lin["w2"], n_heads, device=device)
+
+    @classmethod
+    def from_arrays(cls, ln: dict, lin: dict, n_heads: int, device=None) -> "EsmcBlock":
+        """From LN parameters by name and {name: (codes uint8 [N, K], scales, biases)}."""
+        q = {n: Q8Linear(*lin[n], device=device) for n in LINEARS}
+        return cls(ln["ln1_w"], ln["ln1_b"], ln["q_ln"], ln["k_ln"], ln["ln2_w"], ln["ln2_b"], q["wqkv"], q["wo"],
+                   q["w1"], q["w2"], n_heads, device=device)
+
+    def params(self) -> dict:
+        """The layer's arrays under the reference's names (inverse of ``from_params``)."""
+        p = {n: getattr(self, n).detach().cpu() for n in ("ln1_w", "ln1_b", "q_ln", "k_ln", "ln2_w", "ln2_b")}
+        for n in LINEARS:
+            lin = getattr(self, n)
+            q = lin.q.detach().cpu().contiguous()
+            p[n] = q.view(torch.int32).view(torch.uint32) if hasattr(torch, "uint32") else q.view(torch.int32)
+            p[n + "_s"], p[n + "_b"] = lin.scales.detach().cpu(), lin.biases.detach().cpu()
+        return p
+
+    def attention(self, x: torch.Tensor, h: torch.Tensor, sid, res_scale: float, x_mid: torch.Tensor,
+                  h2: torch.Tensor) -> None:
+        """x_mid = x + wo(attn(h)) / res_scale; h2 = LN2(x_mid). x [B, L, D] fp32, h = LN1(x) fp16."""
+        B, L, D = x.shape
+        qkv = self.wqkv(h)
+        q, k, v = kernels.esmc_qk_rope(qkv.view(B * L, 3 * D), self.q_ln, self.k_ln, EPS, B, L, self.n_heads)
+        o = kernels.esmc_attention(q, k, v, sid)
+        y = self.wo(o)
+        kernels.esmc_layer_norm(x, self.ln2_w, self.ln2_b, EPS, y=y, alpha=1.0 / res_scale, x_out=x_mid, out=h2)
+
+    def ffn(self, h2: torch.Tensor) -> torch.Tensor:
+        """w2(silu(x1) * x2) with [x1 | x2] = w1(h2), fp16 (before the residual's / res_scale)."""
+        return self.w2(kernels.esmc_swiglu(self.w1(h2)))
+
+    def forward(self, x: torch.Tensor, sequence_id=None, res_scale: float = 1.0) -> torch.Tensor:
+        """One block on an fp32 residual [B, L, D] (the reference's block_forward, mlx_esmc.py:84-102)."""
+        x = x.to(torch.float32).contiguous()
+        h = kernels.esmc_layer_norm(x, self.ln1_w, self.ln1_b, EPS)
+        x_mid, h2 = torch.empty_like(x), torch.empty_like(h)
+        self.attention(x, h, _chain_ids(sequence_id, x.device), res_scale, x_mid, h2)
+        out = torch.empty_like(x)
+        # out = x_mid + y2 / res_scale (the LN output of this call is not needed)
+        kernels.esmc_layer_norm(x_mid, self.ln1_w, self.ln1_b, EPS, y=self.ffn(h2), alpha=1.0 / res_scale,
+                                x_out=out, out=torch.empty_like(h))
+        return out
+
+
+def _chain_ids(sequence_id, device):
+    """int32 [B, L] chain ids for the attention mask, or None when every token may attend to
+    every other (a single chain: the reference skips the mask, mlx_esmc.py:188-191)."""
+    if sequence_id is None:
+        return None
+    sid = sequence_id.to(device=device)
+    if bool((sid == sid[:, :1]).all()):
+        return None
+    return sid.to(torch.int32).contiguous()
+
+
+class HipEsmc(nn.Module):
+    """ESMC on the HIP kernels with 8-bit linears: forward(input_ids, sequence_id,
+    output_hidden_states) -> .hidden_states [n_layers + 1, B, L, D] fp32 on the GPU (each
+    block's input, then the final LayerNorm), the contract of MLXEsmc (mlx_esmc.py:179-200)."""
+
+    def __init__(self, embed: torch.Tensor, layers, norm_w: torch.Tensor, n_heads: int = 40, device=None):
+        super().__init__()
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.register_buffer("embed", embed.detach().to(device=dev, dtype=torch.float32).contiguous())
+        self.register_buffer("norm_w", norm_w.detach().to(device=dev, dtype=torch.float32).contiguous())
+        self.layers = nn.ModuleList(layers)
+        self.n_heads = n_heads
+        self.res_scale = math.sqrt(len(layers) / 36)  # mlx_esmc.py:108
+
+    # ---- construction: the reference's converted-weight cache (mlx_esmc.py:116-148) -------------
+    @classmethod
+    def from_cache(cls, path, n_heads: int = 40, device=None) -> "HipEsmc":
+        """From a safetensors file with the reference's layout: "embed", "norm_w" and
+        "layers.{i}.{name}" for every name of ``EsmcBlock.from_params`` (8-bit caches)."""
+        from safetensors.torch import load_file
+        flat = load_file(str(path))
+        n = 1 + max(int(k.split(".")[1]) for k in flat if k.startswith("layers."))
+        per = [{} for _ in range(n)]
+        for k, v in flat.items():
+            if k.startswith("layers."):
+                _, i, name = k.split(".", 2)
+                per[int(i)][name] = v
+        layers = [EsmcBlock.from_params(p, n_heads, device=device) for p in per]
+        return cls(flat["embed"], layers, flat["norm_w"], n_heads, device=device)
+
+    def save_cache(self, path) -> None:
+        from safetensors.torch import save_file
+        flat = {"embed": self.embed.detach().cpu(), "norm_w": self.norm_w.detach().cpu()}
+        for i, blk in enumerate(self.layers):
+            flat.update({f"layers.{i}.{k}": v.contiguous() for k, v in blk.params().items()})
+        save_file(flat, str(path))
+
+    def nbytes(self) -> int:
+        return sum(b.numel() * b.element_size() for b in self.buffers())
+
+    # nn.Module API the fold calls on its ESMC; the weights stay where they are.
+    def to(self, *a, **k):
+        return self
+
+    # ---- forward ---------------------------------------------------------------------------------
+    def hidden_states(self, input_ids: torch.Tensor, sequence_id=None) -> torch.Tensor:
+        dev = self.embed.device
+        ids = input_ids.to(dev)
+        B, L = ids.shape
+        n, D = len(self.layers), self.embed.shape[1]
+        hs = torch.empty(n + 1, B, L, D, dtype=torch.float32, device=dev)
+        hs[0] = self.embed[ids]
+        sid = _chain_ids(sequence_id, dev)
+        h = kernels.esmc_layer_norm(hs[0], self.layers[0].ln1_w, self.layers[0].ln1_b, EPS)
+        h2 = torch.empty_like(h)
+        x_mid = torch.empty(B, L, D, dtype=torch.float32, device=dev)
+        x_last = torch.empty_like(x_mid)
+        for i, blk in enumerate(self.layers):
+            blk.attention(hs[i], h, sid, self.res_scale, x_mid, h2)
+            y2 = blk.ffn(h2)
+            if i + 1 < n:  # second residual into hidden_states[i+1], fused with the next input LN
+                nxt = self.layers[i + 1]
+                kernels.esmc_layer_norm(x_mid, nxt.ln1_w, nxt.ln1_b, EPS, y=y2, alpha=1.0 / self.res_scale,
+                                        x_out=hs[i + 1], out=h)
+            else:  # the last block's output is only seen through the final norm (weights only)
+                kernels.esmc_layer_norm(x_mid, self.norm_w, None, EPS, y=y2, alpha=1.0 / self.res_scale,
+                                        x_out=x_last, out=hs[n], fp32_out=True)
+        return hs
+
+    def forward(self, input_ids=None, sequence_id=None, output_hidden_states=True, **_):
+        return SimpleNamespace(hidden_states=self.hidden_states(input_ids, sequence_id))

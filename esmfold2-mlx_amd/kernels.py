@@ -110,6 +110,59 @@ def transition(z, ln_w, ln_b, eps, w1, w3, w2=None, out=None):
     return out
 
 
+def esmc_layer_norm(x, w, b, eps, y=None, alpha: float = 1.0, x_out=None, out=None, fp32_out: bool = False):
+    """LN over the last axis of the fp32 residual x [M, D] (after x_out = x + alpha*y when y
+    is given) -> fp16 (or fp32) ``out``. Returns out."""
+    lib = capi.lib()
+    _dev(x, "x", torch.float32)
+    M, D = x.shape[0] if x.dim() == 2 else x.numel() // x.shape[-1], x.shape[-1]
+    if y is not None:
+        _dev(y, "y", F16)
+        x_out = x if x_out is None else _dev(x_out, "x_out", torch.float32)
+    dt = torch.float32 if fp32_out else F16
+    out = torch.empty(x.shape, dtype=dt, device=x.device) if out is None else _dev(out, "out", dt)
+    capi.check(lib.esmc_layer_norm(x.data_ptr(), _ptr(y), float(alpha), _ptr(x_out), _dev(w, "w", torch.float32).data_ptr(),
+                                   None if b is None else _dev(b, "b", torch.float32).data_ptr(), float(eps),
+                                   None if fp32_out else out.data_ptr(), out.data_ptr() if fp32_out else None, M, D,
+                                   capi.stream_ptr()))
+    return out
+
+
+def esmc_qk_rope(qkv, q_ln, k_ln, eps, B: int, L: int, n_heads: int, base: float = 10000.0, out=None):
+    """qkv [B*L, 3D] fp16 -> (q, k, v) [B, H, L, 64] fp16 (QK-LayerNorm + NeoX RoPE on q, k)."""
+    lib = capi.lib()
+    _dev(qkv, "qkv", F16)
+    shape = (B, n_heads, L, 64)
+    q, k, v = out if out is not None else tuple(torch.empty(shape, dtype=F16, device=qkv.device) for _ in range(3))
+    capi.check(lib.esmc_qk_rope(qkv.data_ptr(), _dev(q_ln, "q_ln", torch.float32).data_ptr(),
+                                _dev(k_ln, "k_ln", torch.float32).data_ptr(), float(eps), q.data_ptr(), k.data_ptr(),
+                                v.data_ptr(), B, L, n_heads, 64, float(base), capi.stream_ptr()))
+    return q, k, v
+
+
+def esmc_attention(q, k, v, sequence_id=None, scale: float | None = None, out=None):
+    """softmax(q k^T * scale, same-chain mask) v: q, k, v [B, H, L, 64] fp16 -> o [B, L, H*64] fp16."""
+    lib = capi.lib()
+    B, H, L, hd = q.shape
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _dev(t, n, F16)
+    sid = None if sequence_id is None else _dev(sequence_id, "sequence_id", torch.int32)
+    o = torch.empty(B, L, H * hd, dtype=F16, device=q.device) if out is None else _dev(out, "out", F16)
+    capi.check(lib.esmc_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(sid), o.data_ptr(), B, L, H, hd,
+                                  float(hd ** -0.5 if scale is None else scale), capi.stream_ptr()))
+    return o
+
+
+def esmc_swiglu(x12, out=None):
+    """[M, 2F] fp16 (rows [x1 | x2]) -> silu(x1) * x2 [M, F] fp16."""
+    lib = capi.lib()
+    _dev(x12, "x12", F16)
+    M, F2 = x12.shape[0] if x12.dim() == 2 else x12.numel() // x12.shape[-1], x12.shape[-1]
+    y = torch.empty(*x12.shape[:-1], F2 // 2, dtype=F16, device=x12.device) if out is None else _dev(out, "out", F16)
+    capi.check(lib.esmc_swiglu(x12.data_ptr(), y.data_ptr(), M, F2 // 2, capi.stream_ptr()))
+    return y
+
+
 def q8_workspace_bytes(M: int, K: int, N: int) -> int:
     """Bytes of workspace q8_linear uses to split K at this shape (0: it runs unsplit)."""
     return int(capi.lib().q8_linear_workspace_bytes(M, K, N))

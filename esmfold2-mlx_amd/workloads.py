@@ -12,6 +12,11 @@ seeded draws; both sides of a comparison see identical bytes.
   W1 [H, C] ~ N(0, 1/C), W3 [C, H] ~ N(0, 1/H) (ReLU MLP, no biases, LN gamma 1 beta 0).
 * ``q8_inputs``: x [M, K] fp16 ~ N(0, 1); codes q [N, K] ~ U{0..255}; scales
   s [N, K/64] ~ U(0.001, 0.01) and biases b ~ N(0, 0.1), fp16; drawn in that order.
+* ``esmc_block_inputs``: one ESMC block (width D, FFN width F): x [B, L, D] ~ N(0, 1)
+  fp32, LN parameters 1 + N(0, 0.01) and N(0, 0.01), and 8-bit linears wqkv [3D, D],
+  wo [D, D], w1 [2F, D], w2 [D, F] with codes U{0..255} and per-group
+  s = 2a/255 * U(0.9, 1.1), b = -a * U(0.9, 1.1), a = sqrt(3/K): dequantised weights of
+  variance about 1/K, so activations keep unit scale through the block.
 """
 
 from __future__ import annotations
@@ -93,6 +98,28 @@ def block_stack(L: int, n_blocks: int = 8, C: int = 128, c: int = 128, H: int = 
     blocks = [(tmu_params(g, C, c, True), tmu_params(g, C, c, False), transition_params(g, C, H))
               for _ in range(n_blocks)]
     return z, blocks
+
+
+def q8_layer(gen: torch.Generator, N: int, K: int, group: int = 64):
+    """(q uint8 [N, K], s, b fp16 [N, K/group]) with dequantised weights of variance ~1/K."""
+    a = (3.0 / K) ** 0.5
+    q = torch.randint(0, 256, (N, K), generator=gen, dtype=torch.int64).to(torch.uint8)
+    u = lambda: 0.9 + 0.2 * torch.rand(N, K // group, generator=gen, dtype=torch.float32)  # noqa: E731
+    s = (2 * a / 255 * u()).half()
+    b = (-a * u()).half()
+    return q, s, b
+
+
+def esmc_block_inputs(L: int, D: int = 2560, F: int = 5120, B: int = 1, seed: int = 0):
+    """(x [B, L, D] fp32, LN params dict, {name: (q, s, b)} for wqkv, wo, w1, w2)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, L, D, generator=g, dtype=torch.float32)
+    ln = {n: (1.0 if n in ("ln1_w", "q_ln", "k_ln", "ln2_w") else 0.0) +
+          0.1 * torch.randn(D, generator=g, dtype=torch.float32)
+          for n in ("ln1_w", "ln1_b", "q_ln", "k_ln", "ln2_w", "ln2_b")}
+    lin = {"wqkv": q8_layer(g, 3 * D, D), "wo": q8_layer(g, D, D), "w1": q8_layer(g, 2 * F, D),
+           "w2": q8_layer(g, D, F)}
+    return x, ln, lin
 
 
 def q8_inputs(M: int, K: int, N: int, seed: int = 0, group: int = 64):

@@ -205,6 +205,35 @@ size_t q8_packed_scales_bytes(int N, int K);
 int q8_pack_scales(const esm_half* s, const esm_half* b, uint32_t* sb, int N, int K, int group, void* stream);
 
 /*
+ * The ESMC transformer block's other kernels (mlx_esmc.py:84-102), around q8_linear.
+ *
+ * esmc_layer_norm: with y, x_out = x + alpha * y (fp32 residual, y fp16: the scaled
+ *   residual adds `x + (wo(o) / res_scale)`, mlx_esmc.py:97, :102); then
+ *   h = LN(x_out or x; w, b, eps) in fp32, rounded to fp16 (mx.fast.layer_norm,
+ *   :91, :98), or kept in fp32 in h_fp32 (the final norm, :195); exactly one of h,
+ *   h_fp32 is given. x, x_out [M, D] fp32 (x_out may be x); y, h [M, D] fp16;
+ *   w, b [D] fp32 (b may be NULL). D % 8 == 0, D <= 8192.
+ * esmc_qk_rope: qkv [B*L, 3D] fp16 (the wqkv output, rows [q | k | v]); QK-LayerNorm
+ *   over the full width D with weights only (:93-94), fp32 statistics; NeoX rotary
+ *   embedding (mx.fast.rope traditional=False, base rope_base, positions 0..L-1,
+ *   :96-97); q, k, v written head-major [B, H, L, 64] fp16. head_dim = 64, D <= 4096.
+ * esmc_attention: o = softmax(q k^T * scale, mask) v per (batch, head) (:98,
+ *   mx.fast.scaled_dot_product_attention), with token i attending to j iff
+ *   sequence_id[b, i] == sequence_id[b, j] (:186-191; NULL = no mask); fp32 scores and
+ *   softmax, probabilities rounded to fp16 for the second product; o [B, L, H*64] fp16.
+ *   head_dim = 64, L <= 512.
+ * esmc_swiglu: y = silu(x1) * x2 with x12 = [x1 | x2] rows [M, 2F] fp16 (:100-101), in
+ *   fp32, one rounding; y [M, F]. F % 8 == 0.
+ */
+int esmc_layer_norm(const float* x, const esm_half* y, float alpha, float* x_out, const float* w, const float* b,
+                    float eps, esm_half* h, float* h_fp32, int M, int D, void* stream);
+int esmc_qk_rope(const esm_half* qkv, const float* q_ln, const float* k_ln, float eps, esm_half* q, esm_half* k,
+                 esm_half* v, int B, int L, int n_heads, int head_dim, float rope_base, void* stream);
+int esmc_attention(const esm_half* q, const esm_half* k, const esm_half* v, const int* sequence_id, esm_half* o, int B,
+                   int L, int n_heads, int head_dim, float scale, void* stream);
+int esmc_swiglu(const esm_half* x12, esm_half* y, int M, int F, void* stream);
+
+/*
  * Dequantise only: w[n, k] = RN_fp16(s[n, k/group] * q[n, k] + b[n, k/group]),
  * the exact weights q8_linear multiplies by (for the bit-exact check).
  * q [N, K] uint8; s, b [N, K/group] fp16; w [N, K] fp16. group = 64, K % 64 == 0.

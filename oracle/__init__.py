@@ -1,4 +1,4 @@
-"""CPU oracle for the triangle multiplicative update and the 8-bit ESMC linear.
+"""CPU oracle for the triangle multiplicative update, the pair trunk and the 8-bit ESMC linear.
 
 THIS PACKAGE IS TEST INFRASTRUCTURE. It is a CPU restatement of the reference's
 arithmetic, used only as the checker: by ``tests/``, by
@@ -11,6 +11,8 @@ Modules:
                 contraction, LayerNorm, the pair driver, the block stack.
   q8         -- MLX-affine 8-bit group-64 dequantisation and the q8 linear.
   transition -- the pair transition (ReLU MLP, and the reference's SwiGLU).
+  esmc       -- the ESMC transformer block around the 8-bit linear (QK-LayerNorm,
+                NeoX RoPE, chain-masked attention, SwiGLU, scaled residuals).
 
 Every function cites the reference file:line it restates. Paths are relative
 to the reference repository root (abhi0raj/esmfold2-mlx).

@@ -1,0 +1,152 @@
+"""GPU parity of the ESMC block kernels and modules against the oracle (oracle/esmc.py).
+
+Bars: the row kernels (LayerNorm, QK-LN + RoPE, SwiGLU) within a few fp16 roundings of
+the fp64 oracle; attention and the block within max|err| <= 1e-2 x RMS of the oracle's
+output (the block: of its update x_out - x_in), with the 8-bit weights dequantised to
+fp16 as the GEMM multiplies them.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import esmc as oe
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+D64 = torch.float64
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+@pytest.mark.parametrize("D,resid,fp32_out", [(256, False, False), (2560, True, False), (2560, True, True),
+                                              (640, False, True)])
+def test_layer_norm(gpu_lib, pkg, D, resid, fp32_out):
+    g = _gen(D)
+    x = 3 * torch.randn(7, D, generator=g) + 1
+    y = torch.randn(7, D, generator=g).half() if resid else None
+    w, b = 1 + 0.1 * torch.randn(D, generator=g), 0.1 * torch.randn(D, generator=g)
+    xd = x.to(DEV)
+    out = pkg.kernels.esmc_layer_norm(xd, w.to(DEV), b.to(DEV), 1e-5, y=None if y is None else y.to(DEV),
+                                      alpha=0.5, fp32_out=fp32_out)
+    xr = x.double() + (0.5 * y.double() if resid else 0)
+    ref = F.layer_norm(xr, (D,), w.double(), b.double(), 1e-5)
+    tol = (2e-6 if fp32_out else 2 ** -10) * float(ref.abs().max())
+    assert float((out.double().cpu() - ref).abs().max()) <= tol
+    if resid:  # the residual written back in place
+        assert float((xd.double().cpu() - xr).abs().max()) <= 1e-6 * float(xr.abs().max())
+
+
+@pytest.mark.parametrize("B,L,H", [(1, 1, 2), (2, 37, 4), (1, 238, 40)])
+def test_qk_rope(gpu_lib, pkg, B, L, H):
+    D = 64 * H
+    g = _gen(L)
+    qkv = torch.randn(B * L, 3 * D, generator=g).half()
+    qln, kln = 1 + 0.1 * torch.randn(D, generator=g), 1 + 0.1 * torch.randn(D, generator=g)
+    q, k, v = pkg.kernels.esmc_qk_rope(qkv.to(DEV), qln.to(DEV), kln.to(DEV), 1e-5, B, L, H)
+    x = qkv.double().reshape(B, L, 3 * D)
+    heads = lambda t: t.reshape(B, L, H, 64).transpose(1, 2)  # noqa: E731
+    rq = oe.rope(heads(F.layer_norm(x[..., :D], (D,), qln.double(), None, 1e-5)))
+    rk = oe.rope(heads(F.layer_norm(x[..., D:2 * D], (D,), kln.double(), None, 1e-5)))
+    for got, ref in ((q, rq), (k, rk)):
+        assert float((got.double().cpu() - ref).abs().max()) <= 2 ** -9 * float(ref.abs().max())
+    assert torch.equal(v.cpu(), heads(qkv.reshape(B, L, 3 * D)[..., 2 * D:]).contiguous())
+
+
+@pytest.mark.parametrize("L", [1, 5, 31, 64, 130, 238, 300, 512])
+@pytest.mark.parametrize("masked", [False, True])
+def test_attention(gpu_lib, pkg, L, masked):
+    B, H = 2, 3
+    g = _gen(L + masked)
+    q, k, v = (torch.randn(B, H, L, 64, generator=g).half() for _ in range(3))
+    sid = None
+    if masked:  # two chains and padding (its own chain, -1), per batch element
+        sid = torch.zeros(B, L, dtype=torch.int32)
+        sid[0, L // 2:] = 1
+        sid[1, (2 * L) // 3:] = -1
+    o = pkg.kernels.esmc_attention(q.to(DEV), k.to(DEV), v.to(DEV), None if sid is None else sid.to(DEV))
+    ref = oe.attention(q.double(), k.double(), v.double(), oe.chain_mask(sid), 0.125)
+    ref = ref.transpose(1, 2).reshape(B, L, H * 64)
+    err = float((o.double().cpu() - ref).abs().max())
+    assert err <= 1e-2 * float(ref.pow(2).mean().sqrt()), err
+
+
+def test_swiglu(gpu_lib, pkg):
+    g = _gen(0)
+    x = (2 * torch.randn(9, 2 * 320, generator=g)).half()
+    y = pkg.kernels.esmc_swiglu(x.to(DEV)).double().cpu()
+    xd = x.double()
+    ref = F.silu(xd[:, :320]) * xd[:, 320:]
+    assert float((y - ref).abs().max()) <= 2 ** -10 * float(ref.abs().max())
+
+
+def _weights(D, F_, seed):
+    g = _gen(seed)
+    r = lambda *s: torch.randn(*s, generator=g)  # noqa: E731
+    qz = lambda n, k: oe.quantize(r(n, k) * k ** -0.5)  # noqa: E731
+    return oe.EsmcBlockWeights(1 + 0.1 * r(D), 0.1 * r(D), 1 + 0.1 * r(D), 1 + 0.1 * r(D), 1 + 0.1 * r(D),
+                               0.1 * r(D), qz(3 * D, D), qz(D, D), qz(2 * F_, D), qz(D, F_))
+
+
+def _module_block(pkg, p, n_heads):
+    lin = {n: pkg.q8.Q8Linear(torch.from_numpy(getattr(p, n).q), torch.from_numpy(getattr(p, n).s),
+                              torch.from_numpy(getattr(p, n).b)) for n in ("wqkv", "wo", "w1", "w2")}
+    return pkg.esmc.EsmcBlock(p.ln1_w, p.ln1_b, p.q_ln, p.k_ln, p.ln2_w, p.ln2_b, lin["wqkv"], lin["wo"], lin["w1"],
+                              lin["w2"], n_heads)
+
+
+@pytest.mark.parametrize("D,F_,H,L,masked", [(256, 384, 4, 37, True), (640, 1024, 10, 238, False)])
+def test_block(gpu_lib, pkg, D, F_, H, L, masked):
+    p = _weights(D, F_, seed=D)
+    blk = _module_block(pkg, p, H)
+    g = _gen(1)
+    x = 2 * torch.randn(2, L, D, generator=g)
+    sid = None
+    if masked:
+        sid = torch.zeros(2, L, dtype=torch.int64)
+        sid[0, 20:] = 1
+    rs = math.sqrt(80 / 36)
+    out = blk(x.to(DEV), None if sid is None else sid.to(DEV), res_scale=rs).double().cpu()
+    ref = oe.block_forward(p, x.double(), sid, n_heads=H, res_scale=rs, weights="f16")
+    upd = ref - x.double()
+    err = float((out - ref).abs().max())
+    assert err <= 1e-2 * float(upd.pow(2).mean().sqrt()), err
+
+
+def test_hip_esmc_hidden_states_and_cache(gpu_lib, pkg, tmp_path):
+    D, F_, H, n = 256, 384, 4, 3
+    ps = [_weights(D, F_, seed=10 + i) for i in range(n)]
+    g = _gen(5)
+    embed = torch.randn(33, D, generator=g)
+    norm_w = 1 + 0.1 * torch.randn(D, generator=g)
+    model = pkg.esmc.HipEsmc(embed, [_module_block(pkg, p, H) for p in ps], norm_w, n_heads=H)
+    assert model.to("cpu") is model
+    ids = torch.randint(0, 33, (2, 29), generator=g)
+    sid = torch.zeros(2, 29, dtype=torch.int64)
+    sid[1, 15:] = 1
+    hs = model(input_ids=ids.to(DEV), sequence_id=sid.to(DEV), output_hidden_states=True).hidden_states
+    assert hs.shape == (n + 1, 2, 29, D) and hs.dtype == torch.float32
+    # the oracle: each block's input, then the final LayerNorm (weights only)
+    rs = math.sqrt(n / 36)
+    x = embed.double()[ids]
+    for i, p in enumerate(ps):
+        assert float((hs[i].double().cpu() - x).abs().max()) <= 1e-2 * float(x.pow(2).mean().sqrt()) + 1e-6
+        x = oe.block_forward(p, x, sid, n_heads=H, res_scale=rs, weights="f16")
+    last = F.layer_norm(x, (D,), norm_w.double(), None, 1e-5)
+    assert float((hs[n].double().cpu() - last).abs().max()) <= 1e-2 * float(last.pow(2).mean().sqrt())
+    # the reference's converted-weight cache layout: save, reload, same hidden states
+    path = tmp_path / "esmc_q8.safetensors"
+    model.save_cache(path)
+    from safetensors.torch import load_file
+    flat = load_file(str(path))
+    assert {"embed", "norm_w", "layers.0.wqkv", "layers.0.wqkv_s", "layers.0.wqkv_b", "layers.2.w2_b",
+            "layers.1.q_ln"} <= set(flat)
+    assert flat["layers.0.wqkv"].shape == (3 * D, D // 4) and flat["layers.0.wqkv_s"].dtype == torch.float16
+    again = pkg.esmc.HipEsmc.from_cache(path, n_heads=H)
+    hs2 = again(input_ids=ids.to(DEV), sequence_id=sid.to(DEV)).hidden_states
+    assert torch.equal(hs, hs2)
