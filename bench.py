@@ -15,6 +15,8 @@ Also reported on the same JSON line:
                 at L=238 (time, TFLOP/s, fraction of MFMA peak);
   block_stack   the pair-trunk block stack at L=238: 8 blocks of (T_out, T_in,
                 transition) x 3 recycles with z carried, replayed as one HIP graph;
+  recycle       the recycling step's kernels at L=238: the parcae recurrence, the
+                distogram expected distance (64 bins) and the p95 exit quantile;
   esmc_block    one ESMC transformer block at 238 tokens, D=2560, 40 heads, FFN 5120
                 (its wqkv, wo, w1, w2 8-bit linears and the LN / RoPE / attention /
                 SwiGLU kernels), eager launches;
@@ -81,6 +83,7 @@ def parse():
     ap.add_argument("--no-q8", action="store_true", help="skip the q8 linear figures")
     ap.add_argument("--no-stack", action="store_true", help="skip the transition and block-stack figures")
     ap.add_argument("--no-esmc", action="store_true", help="skip the ESMC block figure")
+    ap.add_argument("--no-recycle", action="store_true", help="skip the recycling-step figures")
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 64 MiB device copy 10 times (counter calibration under rocprofv3)")
@@ -369,6 +372,37 @@ def main():
                               "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
                               "cells_per_s_per_block": L * L * 8 * recycles / t}
         stack_case = (zs, blocks, stack_out)
+
+    if not args.no_recycle:
+        g = torch.Generator().manual_seed(0)
+        zr, zi, rf = (torch.randn(1, L, L, C, generator=g).to(dev) for _ in range(3))
+        lw, lb, av = torch.ones(C, device=dev), torch.zeros(C, device=dev), torch.rand(C, generator=g).to(dev)
+        bm = (torch.randn(C, C, generator=g) * C ** -0.5).half().to(dev)
+        dw, db = (torch.randn(64, C, generator=g) * 0.1).half().to(dev), torch.randn(64, generator=g).to(dev)
+        cen = pkg.recycle.centers_6b(dev)
+        zo = torch.empty_like(zr)
+        ed_prev = K.expected_distance(zr, dw, db, cen)
+        ed = torch.empty_like(ed_prev)
+        qo = torch.empty(1, device=dev)
+        ops = {"parcae_step": lambda: K.parcae_step(zr, zi, rf, lw, lb, 1e-5, av, bm, out=zo),
+               "expected_distance": lambda: K.expected_distance(zo, dw, db, cen, out=ed),
+               "p95_quantile": lambda: K.abs_diff_quantile(ed, ed_prev, 0.95, out=qo)}
+        rres = {}
+        for name, fn in ops.items():
+            for _ in range(3):
+                fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(20):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            rres[name] = {"us": e0.elapsed_time(e1) * 1e3 / 20}
+        pb = 4 * C * L * L * 4  # parcae: read z, z_init, refined, write z (fp32)
+        rres["parcae_step"].update({"gbs": pb / rres["parcae_step"]["us"] / 1e3,
+                                    "hbm_frac": pb / rres["parcae_step"]["us"] / 1e3 / (HBM_PEAK / 1e9)})
+        out["recycle"] = rres
 
     esmc_case = None
     if not args.no_esmc:

@@ -9,6 +9,7 @@ Modules:
   q8               -- Q8Linear: the quantized_matmul(transpose=True, group 64, bits 8) contract
   esmc             -- EsmcBlock and HipEsmc: the ESMC language model around the 8-bit linear
   trunk            -- PairTransition, TrunkBlock and PairTrunk (the FoldingTrunk drop-in)
+  recycle          -- ParcaeLoop (the 6B recycling loop) and its distogram exit signal
   var_hip_trimul   -- the reference-style variant plugin for the TMUs: apply(model)
   var_hip_trunk    -- the variant plugin replacing the whole folding trunk: apply(model)
   workloads        -- seeded synthetic inputs of the benchmark configurations
@@ -16,11 +17,11 @@ Modules:
 
 from . import build, capi  # noqa: F401
 
-__all__ = ["build", "capi", "kernels", "trimul", "q8", "esmc", "trunk", "var_hip_trimul", "var_hip_trunk", "workloads"]
+__all__ = ["build", "capi", "kernels", "trimul", "q8", "esmc", "trunk", "recycle", "var_hip_trimul", "var_hip_trunk", "workloads"]
 
 
 def __getattr__(name):
-    if name in ("kernels", "trimul", "q8", "esmc", "trunk", "var_hip_trimul", "var_hip_trunk", "workloads"):
+    if name in ("kernels", "trimul", "q8", "esmc", "trunk", "recycle", "var_hip_trimul", "var_hip_trunk", "workloads"):
         import importlib
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)

@@ -32,6 +32,9 @@ SIGNATURES = {
     "esmc_qk_rope": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _f32, _vp]),
     "esmc_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _f32, _vp]),
     "esmc_swiglu": (_int, [_vp, _vp, _int, _int, _vp]),
+    "parcae_step": (_int, [_vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _vp]),
+    "distogram_expected_distance": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
+    "abs_diff_quantile": (_int, [_vp, _vp, _sz, _f32, _vp, _vp]),
     "q8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "q8_linear_ws": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
     "q8_linear_workspace_bytes": (_sz, [_int, _int, _int]),

@@ -302,6 +302,45 @@ int esmc_swiglu(const esm_half* x12, esm_half* y, int M, int F, void* stream) {
   return hip_status(esm::launch_esmc_swiglu(H(x12), H(y), (size_t)M, F, (hipStream_t)stream), "esmc_swiglu launch");
 }
 
+int parcae_step(const float* z, const float* z_init, const float* refined, const float* ln_w, const float* ln_b,
+                float eps, const float* a, const esm_half* b_mat, float* z_out, int B, int L, int C, void* stream) {
+  if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "parcae_step: B=%d L=%d must be >= 0", B, L);
+  if (C != 128) return fail(ESM_ERR_UNSUPPORTED, "parcae_step: C=%d (supported: 128)", C);
+  if (B == 0 || L == 0) return ok();
+  const size_t ncells = (size_t)B * L * L;
+  if (ncells * C * 4 >= (1ull << 31)) return fail(ESM_ERR_SHAPE, "parcae_step: B*L*L=%zu cells exceed 2 GB", ncells);
+  if (!z || !z_init || !refined || !ln_w || !ln_b || !a || !b_mat || !z_out)
+    return fail(ESM_ERR_NULL, "parcae_step: NULL pointer");
+  if (!aligned16(z) || !aligned16(z_init) || !aligned16(refined) || !aligned16(z_out) || !aligned16(b_mat))
+    return fail(ESM_ERR_ALIGN, "parcae_step: z, z_init, refined, z_out, b_mat must be 16-byte aligned");
+  const size_t ntiles = (ncells + 31) / 32;
+  esm::ParcaeArgs args{z, z_init, refined, ln_w, ln_b, eps, a, H(b_mat), z_out, ncells, (int)ntiles};
+  const int grid = (int)(ntiles < (size_t)cu_count() ? ntiles : cu_count());
+  return hip_status(esm::launch_parcae_step(args, grid, (hipStream_t)stream), "parcae_step launch");
+}
+
+int distogram_expected_distance(const float* r, const esm_half* w, const float* bias, const float* centers, float* ed,
+                                int B, int L, int C, int nbins, void* stream) {
+  if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "distogram_expected_distance: B=%d L=%d", B, L);
+  if (C != 128 || (nbins != 64 && nbins != 128))
+    return fail(ESM_ERR_UNSUPPORTED, "distogram_expected_distance: C=%d nbins=%d (C 128; 64 or 128 bins)", C, nbins);
+  if (B == 0 || L == 0) return ok();
+  if (L > kMaxL) return fail(ESM_ERR_SHAPE, "distogram_expected_distance: L=%d exceeds %d", L, kMaxL);
+  if (!r || !w || !bias || !centers || !ed) return fail(ESM_ERR_NULL, "distogram_expected_distance: NULL pointer");
+  if (!aligned16(r) || !aligned16(w)) return fail(ESM_ERR_ALIGN, "distogram_expected_distance: r, w must be 16-byte aligned");
+  esm::DistoArgs args{r, H(w), bias, centers, ed, B, L, nbins};
+  const long long tiles = (long long)B * L * ((L + 127) / 128);
+  const int grid = (int)(tiles < 4LL * cu_count() ? tiles : 4LL * cu_count());
+  return hip_status(esm::launch_expected_distance(args, grid, (hipStream_t)stream), "distogram_expected_distance launch");
+}
+
+int abs_diff_quantile(const float* x, const float* y, size_t n, float q, float* out, void* stream) {
+  if (n == 0) return fail(ESM_ERR_SHAPE, "abs_diff_quantile: n must be >= 1");
+  if (!(q >= 0.f && q <= 1.f)) return fail(ESM_ERR_SHAPE, "abs_diff_quantile: q=%g outside [0, 1]", (double)q);
+  if (!x || !out) return fail(ESM_ERR_NULL, "abs_diff_quantile: NULL pointer");
+  return hip_status(esm::launch_abs_diff_quantile(x, y, n, q, out, (hipStream_t)stream), "abs_diff_quantile launch");
+}
+
 size_t q8_packed_scales_bytes(int N, int K) {
   if (N <= 0 || K <= 0 || K % 64 != 0) return 0;
   return (size_t)((N + esm::kQ8TileN - 1) / esm::kQ8TileN) * (K / 64) * esm::kQ8TileN * sizeof(uint32_t);

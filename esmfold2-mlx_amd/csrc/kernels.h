@@ -116,6 +116,29 @@ struct EsmcAttnArgs {
   float scale_log2;     // scale * log2(e)
 };
 
+struct ParcaeArgs {
+  const float* z;         // [cells, C] recurrent state
+  const float* z_init;    // [cells, C]
+  const float* refined;   // [cells, C] (the LM encoder's output)
+  const float* ln_w;      // [C]
+  const float* ln_b;      // [C]
+  float eps;
+  const float* a;         // [C]
+  const half_t* b_mat;    // [C, C] (out, in)
+  float* z_out;           // [cells, C], may be z
+  size_t ncells;
+  int ntiles;
+};
+
+struct DistoArgs {
+  const float* r;         // [B, L, L, C]
+  const half_t* w;        // [nbins, C]
+  const float* bias;      // [nbins]
+  const float* centers;   // [nbins]
+  float* ed;              // [B, L, L]
+  int B, L, nbins;
+};
+
 // Cells per tile of the per-cell kernels (a) and (c).
 constexpr int kCellTile = 64;
 
@@ -126,6 +149,9 @@ hipError_t launch_epilogue(const EpilogueArgs& a, int grid, hipStream_t s);
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s);
 hipError_t launch_transition(const TransitionArgs& a, int grid, hipStream_t s);
 hipError_t launch_esmc_ln(const EsmcLnArgs& a, hipStream_t s);
+hipError_t launch_parcae_step(const ParcaeArgs& a, int grid, hipStream_t s);
+hipError_t launch_expected_distance(const DistoArgs& a, int grid, hipStream_t s);
+hipError_t launch_abs_diff_quantile(const float* x, const float* y, size_t n, float q, float* out, hipStream_t s);
 hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s);
 hipError_t launch_esmc_attention(const EsmcAttnArgs& a, hipStream_t s);
 hipError_t launch_esmc_swiglu(const half_t* x12, half_t* y, size_t M, int F, hipStream_t s);

@@ -163,6 +163,47 @@ def esmc_swiglu(x12, out=None):
     return y
 
 
+def parcae_step(z, z_init, refined, ln_w, ln_b, eps, a, b_mat, out=None):
+    """a * z + LN(z_init + refined) @ B^T: z, z_init, refined [B, L, L, C] fp32; b_mat [C, C] fp16."""
+    lib = capi.lib()
+    for t, n in ((z, "z"), (z_init, "z_init"), (refined, "refined")):
+        _dev(t, n, torch.float32)
+    B, L, _, C = z.shape
+    out = torch.empty_like(z) if out is None else _dev(out, "out", torch.float32)
+    capi.check(lib.parcae_step(z.data_ptr(), z_init.data_ptr(), refined.data_ptr(),
+                               _dev(ln_w, "ln_w", torch.float32).data_ptr(), _dev(ln_b, "ln_b", torch.float32).data_ptr(),
+                               float(eps), _dev(a, "a", torch.float32).data_ptr(), _dev(b_mat, "b_mat", F16).data_ptr(),
+                               out.data_ptr(), B, L, C, capi.stream_ptr()))
+    return out
+
+
+def expected_distance(r, w, bias, centers, out=None):
+    """softmax((r + r^T) @ W^T + bias) . centers per pair: r [B, L, L, C] fp32, w [nbins, C] fp16."""
+    lib = capi.lib()
+    _dev(r, "r", torch.float32)
+    B, L, _, C = r.shape
+    nb = w.shape[0]
+    ed = torch.empty(B, L, L, dtype=torch.float32, device=r.device) if out is None else _dev(out, "out", torch.float32)
+    capi.check(lib.distogram_expected_distance(r.data_ptr(), _dev(w, "w", F16).data_ptr(),
+                                               _dev(bias, "bias", torch.float32).data_ptr(),
+                                               _dev(centers, "centers", torch.float32).data_ptr(), ed.data_ptr(), B, L,
+                                               C, nb, capi.stream_ptr()))
+    return ed
+
+
+def abs_diff_quantile(x, y=None, q: float = 0.95, out=None):
+    """The q-th quantile of |x - y| (|x| when y is None), as torch.quantile: a 1-element fp32 tensor."""
+    lib = capi.lib()
+    _dev(x, "x", torch.float32)
+    if y is not None:
+        _dev(y, "y", torch.float32)
+        if y.numel() != x.numel():
+            raise capi.EsmError(-2, "abs_diff_quantile: x and y differ in size")
+    out = torch.empty(1, dtype=torch.float32, device=x.device) if out is None else _dev(out, "out", torch.float32)
+    capi.check(lib.abs_diff_quantile(x.data_ptr(), _ptr(y), x.numel(), float(q), out.data_ptr(), capi.stream_ptr()))
+    return out
+
+
 def q8_workspace_bytes(M: int, K: int, N: int) -> int:
     """Bytes of workspace q8_linear uses to split K at this shape (0: it runs unsplit)."""
     return int(capi.lib().q8_linear_workspace_bytes(M, K, N))

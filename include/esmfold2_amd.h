@@ -234,6 +234,30 @@ int esmc_attention(const esm_half* q, const esm_half* k, const esm_half* v, cons
 int esmc_swiglu(const esm_half* x12, esm_half* y, int M, int F, void* stream);
 
 /*
+ * The recycling step around the trunk.
+ *
+ * parcae_step: z_out = a * z + LN(z_init + refined; ln_w, ln_b, eps) @ B^T on every
+ *   cell (var_6b_mlx_loop.py:67-71: u = z_init + lm_encoder(lm_z), the "parcae"
+ *   linear recurrence, fp32). z, z_init, refined, z_out [B, L, L, C] fp32 (z_out may be
+ *   z); ln_w, ln_b, a [C] fp32; b_mat [C, C] fp16 (torch [out, in]). LayerNorm in fp32,
+ *   its output and B rounded to fp16 for the MFMA, fp32 accumulation and update. C = 128.
+ * distogram_expected_distance: ed = softmax((r + r^T) @ W^T + bias) . centers per pair
+ *   (var_6b_mlx_loop.py:74-76; var_adaptive_loops.py:41-46), r^T swapping the two
+ *   residue axes. r [B, L, L, C] fp32 (the readout or the coda output); w [nbins, C] fp16
+ *   (the head's weight); bias, centers [nbins] fp32; ed [B, L, L] fp32. The pair sums are
+ *   rounded to fp16 for the MFMA; logits and softmax in fp32. C = 128, nbins 64 or 128.
+ * abs_diff_quantile: out[0] = the q-th quantile of |x - y| (y NULL: of |x|) over n values,
+ *   linear interpolation between the two nearest order statistics, as torch.quantile
+ *   (the exit signal: var_6b_mlx_loop.py:79-85 with q = 0.95, var_adaptive_loops.py:116).
+ *   Exact (order statistics by radix selection). x, y [n] fp32; out one fp32.
+ */
+int parcae_step(const float* z, const float* z_init, const float* refined, const float* ln_w, const float* ln_b,
+                float eps, const float* a, const esm_half* b_mat, float* z_out, int B, int L, int C, void* stream);
+int distogram_expected_distance(const float* r, const esm_half* w, const float* bias, const float* centers, float* ed,
+                                int B, int L, int C, int nbins, void* stream);
+int abs_diff_quantile(const float* x, const float* y, size_t n, float q, float* out, void* stream);
+
+/*
  * Dequantise only: w[n, k] = RN_fp16(s[n, k/group] * q[n, k] + b[n, k/group]),
  * the exact weights q8_linear multiplies by (for the bit-exact check).
  * q [N, K] uint8; s, b [N, K/group] fp16; w [N, K] fp16. group = 64, K % 64 == 0.

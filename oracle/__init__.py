@@ -11,6 +11,8 @@ Modules:
                 contraction, LayerNorm, the pair driver, the block stack.
   q8         -- MLX-affine 8-bit group-64 dequantisation and the q8 linear.
   transition -- the pair transition (ReLU MLP, and the reference's SwiGLU).
+  recycle    -- the parcae recycling step, the distogram expected distance and the
+                p95 exit signal.
   esmc       -- the ESMC transformer block around the 8-bit linear (QK-LayerNorm,
                 NeoX RoPE, chain-masked attention, SwiGLU, scaled residuals).
 
