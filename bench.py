@@ -82,6 +82,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-q8", action="store_true", help="skip the q8 linear figures")
     ap.add_argument("--no-stack", action="store_true", help="skip the transition and block-stack figures")
+    ap.add_argument("--no-block-graph", action="store_true",
+                    help="time the transition kernel but skip the HIP-graph block-stack figure")
     ap.add_argument("--no-esmc", action="store_true", help="skip the ESMC block figure")
     ap.add_argument("--no-recycle", action="store_true", help="skip the recycling-step figures")
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
@@ -348,6 +350,7 @@ def main():
         tfl = 4 * C * (4 * C) * L * L
         out["transition"] = {"us": t * 1e6, "tflops": tfl / t / 1e12, "mfma_frac": tfl / t / MFMA_F16_PEAK,
                              "gbs": 4 * C * L * L / t / 1e9}
+    if not args.no_stack and not args.no_block_graph:
         # the block stack: one HIP graph of 8 blocks x 3 recycles (168 kernels), z reloaded per replay
         recycles = 3
         zbuf = torch.empty(1, L, L, C, dtype=torch.float16, device=dev)

@@ -159,12 +159,14 @@ int tmu_epilogue(const esm_half* x, int ldx, const esm_half* z, const esm_half* 
   if (!(ln_in_eps >= 0.f) || !(ln_mix_eps >= 0.f)) return fail(ESM_ERR_SHAPE, "tmu_epilogue: eps must be >= 0");
   esm::EpilogueArgs e{H(x), ldx, H(z), mask ? H(mask) : nullptr, ln_in_w, ln_in_b, ln_in_eps, ln_mix_w, ln_mix_b,
                       ln_mix_eps, H(w_emit), H(w_gate), H(out), B, L, residual ? 1 : 0, out_mask ? 1 : 0, 0, 0};
-  e.tiles_per_line = (L + esm::kCellTile - 1) / esm::kCellTile;
-  const long long ntiles = (long long)B * L * e.tiles_per_line;
-  if (ntiles > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_epilogue: too many tiles");
-  e.ntiles = (int)ntiles;
-  const long long cap = cu_count();  // one persistent workgroup per CU (1 wave per SIMD)
-  const int grid = (int)(ntiles < cap ? ntiles : cap);
+  // units of 32 cells of one pair row, one per wave per round
+  e.tiles_per_line = (L + esm::kEpiUnit - 1) / esm::kEpiUnit;
+  const long long nunits = (long long)B * L * e.tiles_per_line;
+  if (nunits > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_epilogue: too many units");
+  e.ntiles = (int)nunits;
+  const long long cap = cu_count();  // at most one persistent workgroup per CU
+  const long long want = (nunits + esm::kEpiWaves - 1) / esm::kEpiWaves;
+  const int grid = (int)(want < cap ? want : cap);
   return hip_status(esm::launch_epilogue(e, grid, (hipStream_t)stream), "tmu_epilogue launch");
 }
 

@@ -133,6 +133,11 @@ struct RowStage {
 // Logical 16-byte chunk j (halfs 8j .. 8j+7) of staged row r.
 DEV half8 staged_chunk(const half_t* s, int r, int j) { return ld16(s + r * 128 + 8 * (j ^ (r & 15))); }
 
+// -log2(e): with t = -x log2(e), sigmoid(x) = 1 / (1 + 2^t).
+constexpr float kNegLog2e = -1.4426950408889634f;
+// sigmoid from t = -x log2(e): v_exp_f32, one add, v_rcp_f32.
+DEV float sigmoid_from_t(float t) { return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t)); }
+
 DEV float sigmoidf_fast(float x) {
   // 1 / (1 + e^-x): v_exp_f32 and v_rcp_f32 (about 1 ulp each); saturates
   // cleanly to 0 and 1 at +-inf.

@@ -4,17 +4,26 @@
 //
 // Both operands are row-major with k contiguous (the incoming direction arrives
 // pre-transposed from kernel (a)), so every MFMA fragment is one 16-byte LDS read.
-// A workgroup computes a 128 (i) x 256 (j) output block: for L <= 256 that is a
-// whole row block of one channel, so each channel's B is requested by only
-// ceil(L/128) workgroups and A exactly once. Four waves in a 2x2 arrangement
-// each own 64x128 outputs (2x4 MFMA 32x32x16 tiles, 128 accumulators).
-// K advances in steps of 32 through a double-buffered LDS stage fed by 16-byte
-// global loads one step ahead; rows past L and columns past ld are zero-filled
-// at load time.
+// A workgroup computes a 128 (i) x 128 (j) output block; four waves in a 2x2
+// arrangement each own 64x64 outputs (2x2 MFMA 32x32x16 tiles, 64 accumulators).
+// Two workgroups share a CU (73.7 KB of LDS each), so one's operand stream overlaps
+// the other's start-up and output stores: with a single workgroup per CU those
+// phases ran back to back and took ~40% of the kernel.
+//
+// The kernel is bound by how fast one CU can pull operands through its L1 miss path,
+// so the pipeline keeps two 32 KB stages in flight per workgroup: K advances in steps
+// of 64 (each operand row contributes one whole 128-byte line per stage), stage kt+2
+// is requested into registers while stage kt is multiplied out of LDS and stage kt+1
+// (already in registers) is written to the other LDS buffer. Rows past L and columns
+// past ld are zero-filled at load time.
+//
+// Each MFMA computes the transposed tile (B rows as the "A" operand), so every lane
+// ends with 4 consecutive j of one i: the result is staged with 8-byte LDS writes and
+// leaves as whole 16-byte row chunks.
 //
 // Workgroup order is XCD-aware: the dispatcher deals workgroup ids round-robin to
-// the 8 XCDs, so ids are remapped so that consecutive logical blocks (the row
-// blocks of one channel, which read the same B) run on the same XCD and share
+// the 8 XCDs, so ids are remapped so that consecutive logical blocks (the blocks of
+// one channel, which read the same A rows and B rows) run on the same XCD and share
 // its L2.
 #include "common.h"
 #include "kernels.h"
@@ -23,18 +32,22 @@ namespace esm {
 
 namespace {
 constexpr int BM = 128;            // rows (i) per block
-constexpr int BN = 256;            // cols (j) per block
-constexpr int BK = 32;             // k per stage
-constexpr int KS = BK + 8;         // LDS row stride (halfs) of an operand stage
+constexpr int BN = 128;            // cols (j) per block
+constexpr int BK = 64;             // k per stage: one 128-byte line per operand row
+constexpr int KC = BK / 8;         // 16-byte chunks per row per stage
+constexpr int KS = BK + 8;         // LDS row stride (halfs): 36 dwords, 16 consecutive rows
+                                   // start in 16 distinct 4-bank groups
 constexpr int STAGE = (BM + BN) * KS;
 constexpr int CS = BN + 8;         // LDS row stride (halfs) of the output staging tile
 constexpr int SMEM = (2 * STAGE > BM * CS) ? 2 * STAGE : BM * CS;
-constexpr int CHUNKS = (BM + BN) * BK / 8 / 256;  // 16-byte loads per thread per stage
-static_assert((BM + BN) * BK / 8 % 256 == 0, "stage must split evenly over 256 threads");
-static_assert(BM * 4 % 256 == 0, "A chunks must fill whole loader passes");
+constexpr int NT = 256;            // threads per workgroup
+constexpr int CHUNKS = (BM + BN) * KC / NT;  // 16-byte loads per thread per stage
+constexpr int ACHUNKS = BM * KC / NT;        // of which A rows
+static_assert((BM + BN) * KC % NT == 0 && BM * KC % NT == 0, "stage must split evenly over the threads");
+static_assert(2 * SMEM * 2 <= 160 * 1024, "LDS budget: two workgroups per CU");
 }  // namespace
 
-__global__ __launch_bounds__(256, 2) void tmu_contract_kernel(ContractArgs p) {
+__global__ __launch_bounds__(NT, 2) void tmu_contract_kernel(ContractArgs p) {
   __shared__ __align__(16) half_t smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -49,85 +62,101 @@ __global__ __launch_bounds__(256, 2) void tmu_contract_kernel(ContractArgs p) {
   const int cb = (t / nrb) % ncb;
   const int ch = t / (nrb * ncb);
   const int i0 = rb * BM, j0 = cb * BN;
-  // Operand rows i0.. of A and j0.. of B; lanes past L or ld, and the prefetch past the
-  // last stage, use an out-of-range offset: zeros, no memory traffic, no branch.
+  // Operand rows i0.. of A and j0.. of B; lanes past L or ld, and the prefetches past
+  // the last stage, use an out-of-range offset: zeros, no memory traffic, no branch.
   const rsrc_t rA = make_rsrc(p.a + ((size_t)ch * L + i0) * ld);
   const rsrc_t rB = make_rsrc(p.b + ((size_t)ch * L + j0) * ld);
   const int nk = (ld + BK - 1) / BK;
 
-  half8 pre[CHUNKS];
-  auto gload = [&](int kt) {
+  auto gload = [&](half8 (&pre)[CHUNKS], int kt) {
 #pragma unroll
     for (int u = 0; u < CHUNKS; u++) {
-      const int id = tid + 256 * u;
-      const bool isA = u < BM * 4 / 256;  // a compile-time split: chunks 0..BM*4-1 are A rows
-      const int r = isA ? id >> 2 : (id - BM * 4) >> 2;
-      const int k = kt * BK + (id & 3) * 8;
-      const bool ok = kt < nk && (isA ? i0 : j0) + r < L && k < ld;
+      const int id = tid + NT * u;
+      const bool isA = u < ACHUNKS;  // compile-time split: A rows first, then B rows
+      const int r = isA ? id / KC : (id - BM * KC) / KC;
+      const int k = kt * BK + (id % KC) * 8;
+      const bool ok = (isA ? i0 : j0) + r < L && k < ld;  // k >= ld past the last stage
       pre[u] = bload16(isA ? rA : rB, ok ? (uint32_t)(r * ld + k) * 2u : kOOB);
     }
   };
-  auto swrite = [&](int buf) {
+  auto swrite = [&](const half8 (&pre)[CHUNKS], int buf) {
 #pragma unroll
     for (int u = 0; u < CHUNKS; u++) {
-      const int id = tid + 256 * u;
-      const int kc = id & 3;
-      const int row = id >> 2;  // A rows 0..BM-1, then B rows follow them in the stage
-      st16(smem + buf * STAGE + row * KS + kc * 8, pre[u]);
+      const int id = tid + NT * u;
+      const int row = id / KC;  // A rows 0..BM-1, then the B rows follow them in the stage
+      st16(smem + buf * STAGE + row * KS + (id % KC) * 8, pre[u]);
     }
   };
 
-  f32x16 acc[2][4];
+  constexpr int NI = BN / 64;  // 32-column tiles per wave
+  f32x16 acc[2][NI];
 #pragma unroll
   for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-    for (int ni = 0; ni < 4; ni++)
+    for (int ni = 0; ni < NI; ni++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.f;
 
-  gload(0);
-  swrite(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt++) {
-    const int buf = kt & 1;
-    gload(kt + 1);  // unconditional: past the last stage it reads nothing
+  auto compute = [&](int buf) {
     const half_t* a_s = smem + buf * STAGE;
     const half_t* b_s = a_s + BM * KS;
 #pragma unroll
     for (int kk = 0; kk < BK / 16; kk++) {
-      half8 af[2], bf[4];
+      half8 af[2], bf[NI];
 #pragma unroll
       for (int mi = 0; mi < 2; mi++)
         af[mi] = ld16(a_s + (wm * 64 + mi * 32 + (lane & 31)) * KS + kk * 16 + 8 * (lane >> 5));
 #pragma unroll
-      for (int ni = 0; ni < 4; ni++)
-        bf[ni] = ld16(b_s + (wn * 128 + ni * 32 + (lane & 31)) * KS + kk * 16 + 8 * (lane >> 5));
+      for (int ni = 0; ni < NI; ni++)
+        bf[ni] = ld16(b_s + (wn * (BN / 2) + ni * 32 + (lane & 31)) * KS + kk * 16 + 8 * (lane >> 5));
 #pragma unroll
       for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-        for (int ni = 0; ni < 4; ni++) acc[mi][ni] = mfma32(af[mi], bf[ni], acc[mi][ni]);
+        for (int ni = 0; ni < NI; ni++) acc[mi][ni] = mfma32(bf[ni], af[mi], acc[mi][ni]);
     }
-    swrite(buf ^ 1);
+  };
+
+  // Two register stages: while stage kt is multiplied, stage kt+1 sits in one register
+  // set (then goes to the other LDS buffer, last read in stage kt-1, before the barrier
+  // that ends this step) and stage kt+2 loads into the other set. Unrolled by two so
+  // the register sets are static; a step past the last stage multiplies zeros.
+  half8 r0[CHUNKS], r1[CHUNKS];
+  gload(r0, 0);
+  gload(r1, 1);
+  swrite(r0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    gload(r0, kt + 2);
+    compute(0);
+    swrite(r1, 1);
+    __syncthreads();
+    gload(r1, kt + 3);
+    compute(1);
+    swrite(r0, 0);
     __syncthreads();
   }
 
-  // Epilogue: scale, round once, stage, 16-byte stores of whole row segments.
+  // Epilogue: scale, round once, stage, 16-byte stores of whole row segments. Lane l
+  // holds, per tile and register group g, x[i = l % 32][j = 8g + 4(l / 32) .. +3].
   half_t* c_s = smem;
 #pragma unroll
   for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-    for (int ni = 0; ni < 4; ni++)
+    for (int ni = 0; ni < NI; ni++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = wm * 64 + mi * 32 + acc_row32(r, lane);
-        const int col = wn * 128 + ni * 32 + (lane & 31);
-        c_s[row * CS + col] = (half_t)(acc[mi][ni][r] * p.scale);
+      for (int g4 = 0; g4 < 4; g4++) {
+        const int row = wm * 64 + mi * 32 + (lane & 31);
+        const int col = wn * (BN / 2) + ni * 32 + acc_row32(4 * g4, lane);
+        half4 v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = (half_t)(acc[mi][ni][4 * g4 + e] * p.scale);
+        *reinterpret_cast<half4*>(c_s + row * CS + col) = v;
       }
   __syncthreads();
   const rsrc_t rX = make_rsrc(p.x + ((size_t)ch * L + i0) * p.ldx + j0);
 #pragma unroll
-  for (int u = 0; u < (BM * BN / 8) / 256; u++) {
-    const int id = tid + 256 * u;
+  for (int u = 0; u < (BM * BN / 8) / NT; u++) {
+    const int id = tid + NT * u;
     const int row = id / (BN / 8), q = id % (BN / 8);
     const bool ok = i0 + row < L && j0 + q * 8 < p.ldx;
     bstore16(rX, ok ? (uint32_t)(row * p.ldx + q * 8) * 2u : kOOB, ld16(c_s + row * CS + q * 8));

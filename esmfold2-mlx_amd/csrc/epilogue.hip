@@ -2,26 +2,34 @@
 // contraction output -> proj_emit (MFMA) -> * sigmoid(proj_gate(LN_in(z))) (MFMA)
 // [-> * mask] [-> + z], written cell-major.
 //
-// Persistent like kernel (a): one 8-wave workgroup per CU (2 waves per SIMD). Wave w
-// owns output channels [32 (w%4), +32) for cells [32 (w/4), +32) of each tile and keeps
-// those rows of proj_emit and proj_gate in VGPRs as MFMA A-fragments. A tile is 64
-// cells of one row i of the pair grid, cells (i, pos0..pos0+63). Per tile:
-//   1. x[:, i, pos0:pos0+64] arrives as 128 channel rows of 128 contiguous bytes and
-//      is transposed into an LDS tile [cell][c]; its 16-byte chunks are XOR-swizzled
-//      per row so both the transposing 2-byte writes and the 16-byte MFMA reads are
-//      free of bank conflicts;
-//   2. z's 64 cells (256 contiguous bytes each) are LayerNormed (norm_start) into a
-//      second tile; the raw z stays in registers for the residual;
-//   3. norm_mix is applied in place to the x tile (fp32 statistics);
+// Persistent, one 8-wave workgroup per CU (two waves per SIMD). proj_emit and
+// proj_gate (64 KB) are staged into LDS once and stay there; after that the waves never
+// synchronise: each wave owns whole units of 32 cells of one pair row i, cells
+// (i, pos0 .. pos0+31), taken in turn from a per-wave sequence (unit
+// blockIdx.x + G * (wave + 8 k)), so a CU's units spread over its four SIMDs.
+//
+// Per unit, in a wave-private 8 KB LDS buffer:
+//   1. x[:, i, pos0:pos0+32] (128 channel rows of 64 contiguous bytes) and z's 32 cells
+//      (256 contiguous bytes each) arrive as coalesced 16-byte loads;
+//   2. x is staged channel-major; ds_read_b64_tr_b16 (gfx950's transposing LDS read: in
+//      each 16-lane group, lane j names a 4-element piece P_j and lane n receives
+//      P_{4e + n/4}[n % 4], e = 0..3) turns it straight into B-fragments (cell =
+//      lane % 32, channels 16 s + 8 (lane / 32) + 0..7, s = 0..7), two reads per
+//      fragment, with no 2-byte transposing writes;
+//   3. z is staged cell-major over it (16-byte chunks XOR-swizzled per cell) and each
+//      lane reads the B-fragment chunks of its cell; z stays staged for the residual;
+//   3. both LayerNorms run in registers on the fragments: a lane holds 64 of its
+//      cell's 128 channels and its partner lane (lane ^ 32) the other 64, so the
+//      statistics are a lane-local sum plus one exchange (fp32, shifted one-pass);
 //   4. D[o][cell] = W_e[o,:] . LN(x)[cell,:] and the gate GEMM on LN(z) with
-//      v_mfma_f32_32x32x16_f16, each split over two K halves so 4 accumulator chains
-//      keep the MFMA pipe full; each lane holds groups of 4 consecutive output channels
-//      of one cell, applies the gate in fp32 and stages the fp32 update in LDS;
-//   5. the update plus z is rounded once and leaves as whole 256-byte cell rows
-//      (scattered 32-byte pieces of rows measured 2x slower).
-// The input tiles are double-buffered; a tile costs three barriers. The output gate
-// is recomputed from z rather than stored by kernel (a): z is 2C bytes per cell, a
-// stored gate would cost a write plus a read of 2C bytes.
+//      v_mfma_f32_32x32x16_f16, A-fragments read from the LDS-resident weights, two
+//      passes of two 32-row output blocks (4 independent accumulator chains each);
+//   5. the gate in fp32, the mask, the residual z (each lane's accumulator rows are 4
+//      consecutive channels of its cell: one 8-byte piece of the staged z, overwritten
+//      in place by the output), one rounding to fp16; stored as whole 256-byte cell
+//      rows (16 lanes x 16 B).
+// The output gate is recomputed from z rather than stored by kernel (a): z is 2C bytes
+// per cell, a stored gate would cost a write plus a read of 2C bytes.
 #include "common.h"
 #include "kernels.h"
 
@@ -30,239 +38,271 @@ namespace esm {
 namespace {
 constexpr int C = 128;          // pair channels (output)
 constexpr int CL = 128;         // latent channels (contraction output)
-constexpr int TM = kCellTile;   // cells per tile
-constexpr int XS = CL;          // LDS row stride (halfs), x tile (swizzled, no padding)
-constexpr int NS = C + 8;       // LDS row stride (halfs), LN(z) tile
-constexpr int OS = C;           // LDS row stride (floats), update staging (swizzled)
-constexpr int NW = 8;           // waves per workgroup
-constexpr int OPW = 32;         // output channels per wave (one 32-row MFMA tile)
-constexpr int CPT = TM * 16 / (NW * 64);         // cells LayerNormed per thread per tile
-constexpr int XPT = CL * (TM / 8) / (NW * 64);   // 16-byte x chunks per thread per tile
-static_assert(C / OPW * (TM / 32) == NW && CPT == 2 && XPT == 2, "tile split assumed below");
+constexpr int U = kEpiUnit;     // cells per unit
+constexpr int NW = kEpiWaves;   // waves per workgroup (two per SIMD)
+static_assert(U == 32, "a unit is one 32-column MFMA tile of cells");
 }  // namespace
 
-// Physical 16-byte chunk of logical chunk k in row r of the x tile. Rows 8q+e with a
-// fixed e (one transposing write instruction) land in 8 distinct chunks, and 16
-// consecutive rows (one MFMA fragment read) in 16 distinct chunks.
-DEV int xs_chunk(int row, int k) {
-  const int f = 2 * ((row & 7) ^ ((row >> 4) & 3)) + ((row >> 3) & 1);
-  return k ^ f;
+// Row stride (halfs) of the cell-major staging (z and the output) and of the staged
+// weights: 272 bytes, so the 16-byte reads of 16 consecutive rows at one chunk hit 16
+// distinct 4-bank groups, and every address is a per-lane base plus an immediate offset
+// (an XOR swizzle would need a live address register per chunk).
+constexpr int RS = C + 8;
+DEV int cs_off(int cell, int k) { return cell * RS + 8 * k; }
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 of the x tile (channel-major, 64-byte rows of 32 cells): this lane
+// names the piece of 4 cells at (channel k0 + j/4, cells n0 + 4 (j % 4)), j = lane % 16;
+// it receives x[k0 + e][n0 + lane % 16] for e = 0..3.
+DEV half4 tr_read(const half_t* xs, int k0, int n0, int lane) {
+  const int j = lane & 15;
+  const half_t* p = xs + (k0 + (j >> 2)) * U + n0 + 4 * (j & 3);
+  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(__attribute__((address_space(3))) half_t*)p);
+  return __builtin_bit_cast(half4, v);
 }
 
-// Float offset of (cell, channel o) in the fp32 update staging tile: 16-byte chunk o/4
-// stored at chunk (o/4) ^ (cell & 15), so the 16-byte writes of 16 consecutive cells hit
-// 16 distinct bank groups.
-DEV int os_off(int cell, int o) { return cell * OS + 4 * ((o >> 2) ^ (cell & 15)) + (o & 3); }
+// LayerNorm of one cell's 128 channels held as MFMA B-fragments: this lane holds channels
+// 16 s + 8 h + e (s = 0..7, e = 0..7, h = lane / 32), the partner lane (lane ^ 32) the
+// other half. Statistics in fp32 in one pass, shifted by K = one channel of the cell
+// (the same for both lanes): sums of d = x - K and d^2, mean = K + E[d],
+// var = E[d^2] - E[d]^2. With |K - mean| of the order of the standard deviation the
+// cancellation in var is that of the two-pass form, and no fp32 copy of the 64 values
+// has to stay live between passes. gamma / beta come from LDS (fp32).
+DEV void ln_frags(half8 (&v)[CL / 16], const float* w, const float* b, float eps, int h) {
+  const float K = __shfl((float)v[0][0], threadIdx.x & 31);
+  float s0 = 0.f, s1 = 0.f, q0 = 0.f, q1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < CL / 16; k++)
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float d0 = (float)v[k][e] - K, d1 = (float)v[k][e + 1] - K;
+      s0 += d0;
+      s1 += d1;
+      q0 = fmaf(d0, d0, q0);
+      q1 = fmaf(d1, d1, q1);
+    }
+  float s = s0 + s1, q = q0 + q1;
+  s += __shfl_xor(s, 32);
+  q += __shfl_xor(q, 32);
+  const float md = s * (1.0f / CL);
+  const float mean = K + md;
+  const float var = fmaxf(fmaf(q, 1.0f / CL, -md * md), 0.f);
+  const float rstd = rsqrtf(var + eps);
+  const float shift = -mean * rstd;
+#pragma unroll
+  for (int k = 0; k < CL / 16; k++) {
+    const int c0 = 16 * k + 8 * h;
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(w + c0), w1 = *reinterpret_cast<const f32x4*>(w + c0 + 4);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(b + c0), b1 = *reinterpret_cast<const f32x4*>(b + c0 + 4);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[k][e] = (half_t)fmaf(fmaf((float)v[k][e], rstd, shift), w0[e], b0[e]);
+      v[k][e + 4] = (half_t)fmaf(fmaf((float)v[k][e + 4], rstd, shift), w1[e], b1[e]);
+    }
+  }
+}
 
-template <bool USE_MASK>
+// The staging buffer is private to the wave and a wave's LDS operations complete in
+// order; this only keeps the compiler from moving LDS accesses across a phase boundary.
+DEV void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <bool USE_MASK, bool RESIDUAL>
 __global__ __launch_bounds__(NW * 64, 1) void tmu_epilogue_kernel(EpilogueArgs p) {
-  __shared__ __align__(16) half_t x_s[2][TM * XS];
-  __shared__ __align__(16) half_t n_s[2][TM * NS];
-  __shared__ __align__(16) float o_s[TM * OS];
-  __shared__ __align__(16) float m_s[2][TM];
+  __shared__ __align__(16) half_t w_s[2 * C * RS];     // proj_emit rows, then proj_gate rows
+  __shared__ __align__(16) half_t b_s[NW][U * RS];     // per-wave staging: x, then z, then the output
+  static_assert(CL * U <= U * RS, "the channel-major x tile fits the staging buffer");
+  __shared__ __align__(16) float lnp_s[4][C];          // ln_in w, b; ln_mix w, b
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps descriptors scalar
   const int L = p.L;
+  const int h = lane >> 5, cell = lane & 31;
   constexpr bool use_mask = USE_MASK;  // out_mask with a mask: the update is multiplied by it
 
-  // Weight A-fragments: row = output channel o = 32 og + lane%32, k = 16 ks + 8 (lane/32) + e.
-  const int og = wave & 3, chalf = wave >> 2;
-  // proj_emit, then proj_gate, stream through LDS (the fp32 staging tile, 32 KB, is free
-  // until the first tile's GEMMs, two barriers into the loop) in coalesced rounds; both
-  // rounds' loads are in flight together.
-  half8 we[CL / 16], wg[C / 16];
-  auto load_weights = [&] {
-    static_assert(C * CL * 2 <= TM * OS * 4 && C * C * 2 <= TM * OS * 4, "a weight fits the staging tile");
-    half_t* w_s = reinterpret_cast<half_t*>(o_s);
-    RowStage<C, NW * 64> r0, r1;
-    r0.load(p.w_emit, tid);
-    r1.load(p.w_gate, tid);
-    const int o = OPW * og + (lane & 31);
-    r0.store(w_s, tid);
-    __syncthreads();
+  // Weights and LayerNorm parameters into LDS once (coalesced 16-byte rounds).
+  {
+    RowStage<C, NW * 64> re, rg;
+    re.load(p.w_emit, tid);
+    rg.load(p.w_gate, tid);
+    if (tid < C) {
+      lnp_s[0][tid] = p.ln_in_w[tid];
+      lnp_s[1][tid] = p.ln_in_b[tid];
+      lnp_s[2][tid] = p.ln_mix_w[tid];
+      lnp_s[3][tid] = p.ln_mix_b[tid];
+    }
 #pragma unroll
-    for (int ks = 0; ks < CL / 16; ks++) we[ks] = staged_chunk(w_s, o, 2 * ks + (lane >> 5));
+    for (int k = 0; k < RowStage<C, NW * 64>::kPer; k++) {
+      const int qq = tid + NW * 64 * k, r = qq >> 4, j = qq & 15;
+      st16(w_s + r * RS + 8 * j, re.v[k]);
+      st16(w_s + (C + r) * RS + 8 * j, rg.v[k]);
+    }
     __syncthreads();
-    r1.store(w_s, tid);
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < C / 16; ks++) wg[ks] = staged_chunk(w_s, o, 2 * ks + (lane >> 5));
-  };
-  const int ch0 = (lane & 15) * 8;
-  float gin[8], bin[8], gmx[8], bmx[8];
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    gin[e] = p.ln_in_w[ch0 + e];
-    bin[e] = p.ln_in_b[ch0 + e];
-    gmx[e] = p.ln_mix_w[ch0 + e];
-    bmx[e] = p.ln_mix_b[ch0 + e];
   }
+  const half_t* we_s = w_s;
+  const half_t* wg_s = w_s + C * RS;
+  half_t* bs = b_s[wave];
 
-  auto coords = [&](int tile, int& bi, int& i, int& pos0) {
-    const int bl = tile / p.tiles_per_line;
-    pos0 = (tile - bl * p.tiles_per_line) * TM;
+  // One unit's global loads: z (4 cells x 256 B per instruction), x (16 channel rows x
+  // 64 B per instruction), the mask. Lanes past L, and a unit past the end, read nothing.
+  struct UnitLoads {
+    half8 z[8], x[8];
+    float m;
+  };
+  auto unit_coords = [&](int u, int& bi, int& i, int& pos0) {
+    const int bl = u / p.tiles_per_line;
+    pos0 = (u - bl * p.tiles_per_line) * U;
     bi = bl / L;
     i = bl - bi * L;
   };
-
-  // Issue one tile's loads: x rows (channel d, 8 positions per chunk), z cells and, with
-  // out_mask, the raw mask. Out-of-range lanes, and the tile past the end that the
-  // pipeline's last prefetch names, read nothing.
-  auto load_tile = [&](int tile, half8 (&xq)[XPT], half8 (&zq)[CPT], uint16_t (&mq)[CPT]) {
-    const bool live = tile < p.ntiles;
+  auto load_unit = [&](int u, UnitLoads& ld) {
+    const bool live = u < p.ntiles;
     int bi, i, pos0;
-    coords(live ? tile : 0, bi, i, pos0);
-    const size_t row_cells = ((size_t)bi * L + i) * L;
-    const int q = lane & 7;
-    const bool okx = live && pos0 + q * 8 < L;
+    unit_coords(live ? u : 0, bi, i, pos0);
+    const size_t row_cells = ((size_t)bi * L + i) * L + pos0;  // first cell of the unit
+    const rsrc_t rz = make_rsrc(p.z + row_cells * C);
 #pragma unroll
-    for (int u = 0; u < XPT; u++) {
-      // this wave's lanes cover channels d = 64u + 8 wave + (lane >> 3), 8 positions each
-      const rsrc_t rx = make_rsrc(p.x + (((size_t)bi * CL + 64 * u + 8 * wave) * L + i) * p.ldx + pos0);
-      xq[u] = bload16(rx, okx ? (uint32_t)((size_t)(lane >> 3) * L * p.ldx + q * 8) * 2u : kOOB);
+    for (int m = 0; m < 8; m++) {
+      const int c = 4 * m + (lane >> 4);
+      ld.z[m] = bload16(rz, live && pos0 + c < L ? (uint32_t)(c * C + (lane & 15) * 8) * 2u : kOOB);
     }
-    const rsrc_t rz = make_rsrc(p.z + (row_cells + pos0) * C);
-    const rsrc_t rm = make_rsrc(use_mask ? (const void*)(p.mask + row_cells + pos0) : (const void*)p.z);
-    (void)rm;
+    const int q = lane & 3;
+    const bool okx = live && pos0 + 8 * q < p.ldx;
 #pragma unroll
-    for (int it = 0; it < CPT; it++) {
-      const int cl = (tid >> 4) + (NW * 4) * it;
-      const bool ok = live && pos0 + cl < L;
-      zq[it] = bload16(rz, ok ? (uint32_t)(cl * C + ch0) * 2u : kOOB);
-      if (use_mask) mq[it] = bload2(rm, ok ? (uint32_t)cl * 2u : kOOB);
+    for (int m = 0; m < 8; m++) {
+      const rsrc_t rx = make_rsrc(p.x + (((size_t)bi * CL + 16 * m) * L + i) * p.ldx + pos0);
+      ld.x[m] = bload16(rx, okx ? (uint32_t)((size_t)(lane >> 2) * L * p.ldx + 8 * q) * 2u : kOOB);
+    }
+    ld.m = 1.f;
+    if (use_mask) {
+      const rsrc_t rm = make_rsrc(p.mask + row_cells);
+      ld.m = h2f(bload2(rm, live && pos0 + cell < L ? (uint32_t)cell * 2u : kOOB));
     }
   };
 
-  auto process_tile = [&](int tile, const half8 (&xq)[XPT], const half8 (&zq)[CPT], const uint16_t (&mq)[CPT],
-                          int nb) {
+  auto process_unit = [&](int u, const UnitLoads& ld) {
     int bi, i, pos0;
-    coords(tile, bi, i, pos0);
-    const size_t row_cells = ((size_t)bi * L + i) * L;
-    half_t* xs = x_s[nb];
-    half_t* ns = n_s[nb];
-    // 1. x chunks -> LDS [cell][d], transposed, swizzled
+    unit_coords(u, bi, i, pos0);
+    const size_t row_cells = ((size_t)bi * L + i) * L + pos0;  // first cell of the unit
+    const int q = lane & 3;
+    const float mv = ld.m;
+    // 2. x: stage channel-major (64-byte rows), transposing reads into B-fragments.
 #pragma unroll
-    for (int u = 0; u < XPT; u++) {
-      const int d = (tid >> 3) + 64 * u, q = tid & 7;
+    for (int m = 0; m < 8; m++) st16(&bs[(16 * m + (lane >> 2)) * U + 8 * q], ld.x[m]);
+    wave_lds_fence();
+    half8 nx[CL / 16];
+    const int n0 = 16 * ((lane >> 4) & 1);
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const int row = q * 8 + e;
-        xs[row * XS + 8 * xs_chunk(row, d >> 3) + (d & 7)] = xq[u][e];
-      }
-    }
-    // 2. LN_in(z) -> LDS (the raw z stays in registers for the residual)
-#pragma unroll
-    for (int it = 0; it < CPT; it++) {
-      const int cl = (tid >> 4) + (NW * 4) * it;
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = (float)zq[it][e];
-      ln_row128(v, gin, bin, p.eps_in);
-      half8 o;
-#pragma unroll
-      for (int e = 0; e < 8; e++) o[e] = (half_t)v[e];
-      st16(&ns[cl * NS + ch0], o);
-      if ((lane & 15) == 0) m_s[nb][cl] = use_mask ? h2f(mq[it]) : 1.f;
-    }
-    __syncthreads();
-
-    // 3. norm_mix in place on the x tile (lane reads logical chunk lane%16 of its cell)
-#pragma unroll
-    for (int it = 0; it < CPT; it++) {
-      const int cl = (tid >> 4) + (NW * 4) * it;
-      half_t* px = &xs[cl * XS + 8 * xs_chunk(cl, lane & 15)];
-      const half8 h = ld16(px);
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = (float)h[e];
-      ln_row128(v, gmx, bmx, p.eps_mix);
-      half8 o;
-#pragma unroll
-      for (int e = 0; e < 8; e++) o[e] = (half_t)v[e];
-      st16(px, o);
-    }
-    __syncthreads();
-
-    // 4. emit and gate GEMMs for this wave's 32 cells and 32 output channels, each K split
-    //    in two (4 independent accumulator chains); gate in fp32; fp32 update -> LDS
-    {
-      const int cell = 32 * chalf + (lane & 31);
-      f32x16 e0, e1, g0, g1;
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        e0[r] = 0.f;
-        e1[r] = 0.f;
-        g0[r] = 0.f;
-        g1[r] = 0.f;
-      }
-#pragma unroll
-      for (int ks = 0; ks < CL / 32; ks++) {
-        const int k1 = ks + CL / 32;
-        e0 = mfma32(we[ks], ld16(&xs[cell * XS + 8 * xs_chunk(cell, 2 * ks + (lane >> 5))]), e0);
-        e1 = mfma32(we[k1], ld16(&xs[cell * XS + 8 * xs_chunk(cell, 2 * k1 + (lane >> 5))]), e1);
-        g0 = mfma32(wg[ks], ld16(&ns[cell * NS + 16 * ks + 8 * (lane >> 5)]), g0);
-        g1 = mfma32(wg[k1], ld16(&ns[cell * NS + 16 * k1 + 8 * (lane >> 5)]), g1);
-      }
-      const float mv = m_s[nb][cell];
-#pragma unroll
-      for (int r4 = 0; r4 < 4; r4++) {
-        f32x4 u;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int r = 4 * r4 + e;
-          u[e] = (e0[r] + e1[r]) * sigmoidf_fast(g0[r] + g1[r]) * mv;
-        }
-        *reinterpret_cast<f32x4*>(&o_s[os_off(cell, OPW * og + acc_row32(4 * r4, lane))]) = u;
-      }
-    }
-    __syncthreads();
-
-    // 5. (+ z from registers), one rounding, whole 256-byte cell rows (16 lanes x 16 B);
-    //    cells past L are dropped by the buffer range check.
-    const rsrc_t ro = make_rsrc(p.out + (row_cells + pos0) * C);
-#pragma unroll
-    for (int it = 0; it < CPT; it++) {
-      const int cl = (tid >> 4) + (NW * 4) * it;
-      const f32x4 u0 = *reinterpret_cast<const f32x4*>(&o_s[os_off(cl, ch0)]);
-      const f32x4 u1 = *reinterpret_cast<const f32x4*>(&o_s[os_off(cl, ch0 + 4)]);
-      half8 o;
+    for (int s = 0; s < CL / 16; s++) {
+      const half4 lo = tr_read(bs, 16 * s + 8 * h, n0, lane);
+      const half4 hi = tr_read(bs, 16 * s + 8 * h + 4, n0, lane);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        float v0 = u0[e], v1 = u1[e];
-        if (p.residual) {
-          v0 += (float)zq[it][e];
-          v1 += (float)zq[it][e + 4];
-        }
-        o[e] = (half_t)v0;
-        o[e + 4] = (half_t)v1;
+        nx[s][e] = lo[e];
+        nx[s][e + 4] = hi[e];
       }
-      bstore16(ro, pos0 + cl < L ? (uint32_t)(cl * C + ch0) * 2u : kOOB, o);
     }
+    wave_lds_fence();
+
+    // 3. z: stage cell-major over x, read the B-fragment chunks of this lane's cell. z
+    //    stays staged for the residual: the output piece of each lane overwrites exactly
+    //    the z piece it adds.
+#pragma unroll
+    for (int m = 0; m < 8; m++) st16(&bs[cs_off(4 * m + (lane >> 4), lane & 15)], ld.z[m]);
+    wave_lds_fence();
+    half8 nz[CL / 16];
+#pragma unroll
+    for (int s = 0; s < C / 16; s++) nz[s] = ld16(&bs[cs_off(cell, 2 * s + h)]);
+
+    // 4. LayerNorms in registers.
+    ln_frags(nz, lnp_s[0], lnp_s[1], p.eps_in, h);
+    ln_frags(nx, lnp_s[2], lnp_s[3], p.eps_mix, h);
+
+    // 5. GEMMs, two passes of two 32-row output blocks; gate, mask, residual, one
+    //    rounding; 8-byte pieces staged cell-major.
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+      f32x16 e[2], g[2];
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          e[t][r] = 0.f;
+          g[t][r] = 0.f;
+        }
+      // A-fragments read per k-step (the other wave on the SIMD covers their latency); the
+      // scheduling barrier keeps the compiler from hoisting every k-step's reads at once.
+#pragma unroll
+      for (int s = 0; s < CL / 16; s++) {
+        half8 wa[2][2];  // [t][emit, gate]
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          const int o = 32 * (2 * pass + t) + cell;
+          wa[t][0] = ld16(we_s + o * RS + 8 * (2 * s + h));
+          wa[t][1] = ld16(wg_s + o * RS + 8 * (2 * s + h));
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          e[t] = mfma32(wa[t][0], nx[s], e[t]);
+          g[t] = mfma32(wa[t][1], nz[s], g[t]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const int ob = 2 * pass + t;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          // channels 32 ob + 8 j + 4 h + 0..3 of this lane's cell: the rows its
+          // accumulators hold, and one 8-byte piece of the staged z
+          half4* piece = reinterpret_cast<half4*>(&bs[cs_off(cell, 4 * ob + j) + 4 * h]);
+          const half4 zr = *piece;
+          half4 o;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            float v = e[t][4 * j + r] * sigmoid_from_t(g[t][4 * j + r] * kNegLog2e);
+            if (use_mask) v *= mv;
+            if (RESIDUAL) v += (float)zr[r];
+            o[r] = (half_t)v;
+          }
+          *piece = o;
+        }
+      }
+    }
+    wave_lds_fence();
+
+    // 6. Whole 256-byte cell rows: 16 lanes x 16 B, 4 cells per store.
+    const rsrc_t ro = make_rsrc(p.out + row_cells * C);
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+      const int c = 4 * m + (lane >> 4);
+      bstore16(ro, pos0 + c < L ? (uint32_t)(c * C + (lane & 15) * 8) * 2u : kOOB, ld16(&bs[cs_off(c, lane & 15)]));
+    }
+    wave_lds_fence();
   };
 
-  // Software pipeline: the next tile's loads fly while this one computes (ping-pong
-  // register buffers, unrolled by two so no register copy waits on a load).
   const int G = gridDim.x;
-  half8 xA[XPT], zA[CPT], xB[XPT], zB[CPT];
-  uint16_t mA[CPT] = {}, mB[CPT] = {};
-  int tile = blockIdx.x;
-  load_tile(tile, xA, zA, mA);  // the first tile's data goes out before the weights
-  load_weights();
-  for (; tile < p.ntiles; tile += 2 * G) {
-    load_tile(tile + G, xB, zB, mB);
-    process_tile(tile, xA, zA, mA, 0);
-    if (tile + G >= p.ntiles) break;
-    load_tile(tile + 2 * G, xA, zA, mA);
-    process_tile(tile + G, xB, zB, mB, 1);
+  for (int u = blockIdx.x + G * wave; u < p.ntiles; u += G * NW) {
+    UnitLoads ld;
+    load_unit(u, ld);
+    process_unit(u, ld);
   }
 }
 
 hipError_t launch_epilogue(const EpilogueArgs& a, int grid, hipStream_t s) {
-  if (a.out_mask && a.mask)
-    hipLaunchKernelGGL(tmu_epilogue_kernel<true>, dim3(grid), dim3(NW * 64), 0, s, a);
+  const bool m = a.out_mask && a.mask;
+  if (m && a.residual)
+    hipLaunchKernelGGL((tmu_epilogue_kernel<true, true>), dim3(grid), dim3(NW * 64), 0, s, a);
+  else if (m)
+    hipLaunchKernelGGL((tmu_epilogue_kernel<true, false>), dim3(grid), dim3(NW * 64), 0, s, a);
+  else if (a.residual)
+    hipLaunchKernelGGL((tmu_epilogue_kernel<false, true>), dim3(grid), dim3(NW * 64), 0, s, a);
   else
-    hipLaunchKernelGGL(tmu_epilogue_kernel<false>, dim3(grid), dim3(NW * 64), 0, s, a);
+    hipLaunchKernelGGL((tmu_epilogue_kernel<false, false>), dim3(grid), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 

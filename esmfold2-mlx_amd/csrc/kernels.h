@@ -141,6 +141,10 @@ struct DistoArgs {
 
 // Cells per tile of the per-cell kernels (a) and (c).
 constexpr int kCellTile = 64;
+// Cells per unit of the epilogue kernel (c): one 32-column MFMA tile of one pair row;
+// waves per epilogue workgroup (two per SIMD).
+constexpr int kEpiUnit = 32;
+constexpr int kEpiWaves = 8;
 
 // Each launcher returns the hipError_t of the launch.
 hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s);
