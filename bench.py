@@ -192,10 +192,10 @@ def main():
     b = torch.empty_like(a)
     x = torch.empty_like(a)
     stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
     scale = 1.0 / 256.0
 
     def launch(kind, m: "pkg.trimul.TriMul", zin, zout):
+        sp = pkg.capi.stream_ptr()  # the current stream: the capture stream while a graph records
         if kind == "project":
             rc = lib.tmu_project(zin.data_ptr(), None, m.ln_in_w.data_ptr(), m.ln_in_b.data_ptr(), m.ln_in_eps,
                                  m.w_bundle.data_ptr(), a.data_ptr(), b.data_ptr(), 1, L, C, CL, ld,

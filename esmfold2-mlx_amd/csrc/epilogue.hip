@@ -6,7 +6,7 @@
 // proj_gate (64 KB) are staged into LDS once and stay there; after that the waves never
 // synchronise: each wave owns whole units of 32 cells of one pair row i, cells
 // (i, pos0 .. pos0+31), taken in turn from a per-wave sequence (unit
-// blockIdx.x + G * (wave + 8 k)), so a CU's units spread over its four SIMDs.
+// 8 blockIdx.x + wave + 8 G k), so a CU's units spread over its four SIMDs.
 //
 // Per unit, in a wave-private 8 KB LDS buffer:
 //   1. x[:, i, pos0:pos0+32] (128 channel rows of 64 contiguous bytes) and z's 32 cells
@@ -285,8 +285,11 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_epilogue_kernel(EpilogueArgs p
     wave_lds_fence();
   };
 
+  // Consecutive units go to the waves of one workgroup: the two 32-cell halves of a
+  // 128-byte line of x are then read on one CU (dealt to different XCDs, each half
+  // fetched the whole line again: 1.8x the compulsory reads).
   const int G = gridDim.x;
-  for (int u = blockIdx.x + G * wave; u < p.ntiles; u += G * NW) {
+  for (int u = blockIdx.x * NW + wave; u < p.ntiles; u += G * NW) {
     UnitLoads ld;
     load_unit(u, ld);
     process_unit(u, ld);
