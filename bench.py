@@ -275,7 +275,7 @@ def main():
     for k, e0, e1 in evs:
         durs[k].append(e0.elapsed_time(e1) * 1e-3)
     for k in kinds:
-        t = statistics.mean(durs[k])
+        t = statistics.median(durs[k])  # robust to a stray slow event pair
         kern[k] = {"us": t * 1e6, "tflops": counts[k]["flops"] / t / 1e12,
                    "gbs": counts[k]["bytes"] / t / 1e9,
                    "mfma_frac": counts[k]["flops"] / t / MFMA_F16_PEAK,

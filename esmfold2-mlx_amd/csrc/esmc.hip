@@ -174,14 +174,25 @@ __global__ __launch_bounds__(256, 1) void esmc_attention_kernel(EsmcAttnArgs p) 
   const half_t* K = p.k + (size_t)bh * L * HD;
   const half_t* V = p.v + (size_t)bh * L * HD;
 
-  // K -> LDS rows, V -> LDS transposed; keys past L are zero
-  for (int c = tid; c < LP * (HD / 8); c += 256) {
-    const int key = c / (HD / 8), d0 = 8 * (c % (HD / 8));
-    const half8 kv = key < L ? ld16(K + (size_t)key * HD + d0) : zero_half8();
-    const half8 vv = key < L ? ld16(V + (size_t)key * HD + d0) : zero_half8();
-    st16(&k_s[key * KSTR + d0], kv);
+  // K -> LDS rows, V -> LDS transposed; keys past L are zero. Every load is issued before
+  // the first LDS write (a rolled loop waited on each iteration's loads in turn).
+  constexpr int NCH = LP * (HD / 8) / 256;  // 16-byte chunks of K (and of V) per thread
+  static_assert(LP * (HD / 8) % 256 == 0, "whole chunks per thread");
+  const rsrc_t rk = make_rsrc(K), rv = make_rsrc(V);
+  half8 kv[NCH], vv[NCH];
 #pragma unroll
-    for (int e = 0; e < 8; e++) vt_s[(d0 + e) * VSTR + key] = vv[e];
+  for (int i = 0; i < NCH; i++) {
+    const int c = tid + 256 * i, key = c / (HD / 8), d0 = 8 * (c % (HD / 8));
+    const uint32_t off = key < L ? (uint32_t)(key * HD + d0) * 2u : kOOB;
+    kv[i] = bload16(rk, off);
+    vv[i] = bload16(rv, off);
+  }
+#pragma unroll
+  for (int i = 0; i < NCH; i++) {
+    const int c = tid + 256 * i, key = c / (HD / 8), d0 = 8 * (c % (HD / 8));
+    st16(&k_s[key * KSTR + d0], kv[i]);
+#pragma unroll
+    for (int e = 0; e < 8; e++) vt_s[(d0 + e) * VSTR + key] = vv[i][e];
   }
   for (int key = tid; key < LP; key += 256) sid_s[key] = key < L ? (p.sid ? p.sid[(size_t)b * L + key] : 0) : -2;
   __syncthreads();

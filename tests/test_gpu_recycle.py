@@ -51,9 +51,10 @@ def test_expected_distance(gpu_lib, pkg, L, nbins):
     assert torch.equal(ed, ed.transpose(1, 2))
 
 
-@pytest.mark.parametrize("n", [1, 2, 3, 1000, 56644, 300000])
+@pytest.mark.parametrize("n", [1, 2, 3, 1000, 56644, 65536, 65537, 300000])
 @pytest.mark.parametrize("q", [0.0, 0.5, 0.95, 1.0])
 def test_abs_diff_quantile(gpu_lib, pkg, n, q):
+    """Against torch.quantile, with ties, at the endpoints and across 2^16 values."""
     g = torch.Generator().manual_seed(n)
     x = torch.randn(n, generator=g) * 3
     y = torch.randn(n, generator=g) * 3
@@ -65,6 +66,15 @@ def test_abs_diff_quantile(gpu_lib, pkg, n, q):
     assert abs(got - ref) <= 1e-6 * max(1.0, abs(ref))
     got1 = float(pkg.kernels.abs_diff_quantile(x.to(DEV), None, q).item())
     assert abs(got1 - float(torch.quantile(x.abs().double(), q))) <= 1e-6 * max(1.0, float(x.abs().max()))
+
+
+@pytest.mark.parametrize("n", [4096, 65536, 70000])
+def test_abs_diff_quantile_one_value(gpu_lib, pkg, n):
+    """Every value but one in a single histogram bin."""
+    x = torch.full((n,), 2.5)
+    x[n // 2] = 7.0
+    got = float(pkg.kernels.abs_diff_quantile(x.to(DEV), None, 0.95).item())
+    assert got == float(torch.quantile(x.double(), 0.95))
 
 
 def _oracle_trunk(blocks):
