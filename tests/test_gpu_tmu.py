@@ -128,6 +128,37 @@ def test_epilogue_kernel(gpu_lib, pkg, L, residual):
         _bar(out, upd)
 
 
+@pytest.mark.parametrize("L", [3, 33, 70])
+@pytest.mark.parametrize("residual", [False, True])
+def test_epilogue_kernel_masked_batch(gpu_lib, pkg, L, residual):
+    """The out_mask variants, two batch entries, rows that end in a partial 32-cell unit;
+    the output may alias z when the residual is added."""
+    B = 2
+    p = _weights(200 + L, True, random_ln=True)
+    g = torch.Generator().manual_seed(1000 + L)
+    z = _z(L + 7, B, L)
+    mask = _mask(L + 3, B, L, "random")
+    ld = pkg.kernels.leading_dim(L)
+    x = torch.zeros(B, 128, L, ld, dtype=torch.float16)
+    x[..., :L] = (2 * torch.randn(B, 128, L, L, generator=g) - 0.5).half()
+    zd = z.to(DEV)
+    out = pkg.kernels.epilogue(x.to(DEV), zd, mask.to(DEV), p.ln_in_w.to(DEV), p.ln_in_b.to(DEV), p.ln_in_eps,
+                               p.ln_mix_w.to(DEV), p.ln_mix_b.to(DEV), p.ln_mix_eps, p.w_emit.half().to(DEV),
+                               p.w_gate.half().to(DEV), residual=residual, out_mask=True,
+                               out=zd if residual else None)
+    torch.cuda.synchronize()
+    pd = _f16_weights(p)
+    n = tmu.layer_norm(z.double(), pd.ln_in_w, pd.ln_in_b, pd.ln_in_eps)
+    xm = x[..., :L].double().permute(0, 2, 3, 1)
+    upd = torch.nn.functional.linear(tmu.layer_norm(xm, pd.ln_mix_w, pd.ln_mix_b, pd.ln_mix_eps), pd.w_emit)
+    upd = upd * torch.sigmoid(torch.nn.functional.linear(n, pd.w_gate)) * mask.double()[..., None]
+    got = out.double().cpu()
+    if residual:
+        got = got - z.double()
+    _bar(got, upd)
+    assert torch.count_nonzero(got[mask == 0]) == 0
+
+
 @pytest.mark.parametrize("L", [1, 2, 5, 17, 64, 76, 127, 129])
 @pytest.mark.parametrize("outgoing", [True, False])
 @pytest.mark.parametrize("mask_kind", [None, "random", "padded"])
