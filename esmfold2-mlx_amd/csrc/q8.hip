@@ -8,14 +8,15 @@
 // same bits as the dequantise entry point.
 //
 // Tiling: a workgroup owns a 64 (m) x 160 (n) tile of y = 2 x 5 blocks of the
-// 32x32x16 MFMA, and a range of K. Its 4 waves (one per SIMD) split that range into
-// contiguous runs of 64-wide groups; each wave accumulates the whole tile (10
-// independent chains) over its run, so every dequantised weight feeds 64 rows of x
-// and no two waves dequantise the same weight. Per group a lane loads 32 codes of
-// each of its 5 weight rows and 32 x values of each of its 2 x rows straight into
-// registers (one group ahead), so the main loop touches no LDS. The K order inside a
-// group is permuted (MFMA step kk takes k = 32*(lane/32) + 8*kk + e) so that a lane's
-// codes and x values are contiguous; A and B use the same order.
+// 32x32x16 MFMA, and a range of K, walked in steps of two 64-wide groups (128 k).
+// Each step's codes (160 rows x 128 B), x (64 rows x 256 B) and packed scales are
+// loaded with row-contiguous 16-byte loads (8 or 16 lanes per row, one step ahead in
+// registers) and stored to one of two LDS stages; one barrier per step. Wave w then
+// takes MFMA step kk = w of both groups: every wave accumulates the whole tile (10
+// independent chains) over its quarter of each step's k, so every dequantised weight
+// feeds 64 rows of x and no two waves dequantise the same weight. (Loading the MFMA
+// fragments straight from global memory instead puts 32 rows in every load
+// instruction, i.e. 32 to 64 cache lines for 1 KB, and measured 1.8x slower.)
 // Weight codes dominate the traffic (1 byte per MAC row); M-tiles of the same n-tile
 // are neighbours in the XCD-aware order and read the codes from one L2.
 //

@@ -8,8 +8,8 @@
 //
 // Persistent, one 4-wave workgroup per CU (one wave per SIMD, up to 512 registers):
 // wave w owns hidden units [wU, wU + U) (U = H/4) and keeps its slices of W1 (and W2)
-// and of W3 in registers for the whole launch (256 registers at H = 512): the MFMA
-// and the VALU do not overlap on a SIMD, so nothing is streamed per tile. Per tile of
+// and of W3 in registers for the whole launch (256 registers at H = 512), so the only
+// per-tile traffic is z in and out and the partials through LDS. Per tile of
 // 32 consecutive cells:
 //   1. LayerNorm (16 lanes per cell) into an LDS tile n[cell][c]; the raw z stays in
 //      registers for the residual;
