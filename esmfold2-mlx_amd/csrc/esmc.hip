@@ -3,8 +3,8 @@
 //   esmc_ln        x' = x + alpha*y (fp32 residual, optional), h = LN(x') -> fp16 or fp32
 //   esmc_qk_rope   QK-LayerNorm over the full width (weight only, fp32 statistics),
 //                  NeoX rotary embedding, head-major q, k, v for the attention
-//   esmc_attention softmax(q k^T * scale, same-chain mask) v, one head per workgroup
-//                  column, MFMA for both products
+//   esmc_attention softmax(q k^T * scale, same-chain mask) v, 32 queries of one head
+//                  per workgroup, keys split over its 4 waves, MFMA for both products
 //   esmc_swiglu    silu(x1) * x2 in fp32, one rounding
 // Row kernels run one 256-thread workgroup per token row (the rows are a few KB: these
 // are launch- and latency-bound, a few microseconds each at 238 tokens).
@@ -27,6 +27,25 @@ DEV float wg_sum(float v, float* red) {
   if ((threadIdx.x & 63) == 0) red[w] = v;
   __syncthreads();
   return red[0] + red[1] + red[2] + red[3];
+}
+
+typedef float float2v __attribute__((ext_vector_type(2)));
+// Two sums over the workgroup at once (one pair of barriers).
+DEV float2v wg_sum2(float a, float b, float (*red)[4]) {
+  a = row16_sum(a);
+  b = row16_sum(b);
+  a += __shfl_xor(a, 16);
+  b += __shfl_xor(b, 16);
+  a += __shfl_xor(a, 32);
+  b += __shfl_xor(b, 32);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();  // red is reused by consecutive calls
+  if ((threadIdx.x & 63) == 0) {
+    red[0][w] = a;
+    red[1][w] = b;
+  }
+  __syncthreads();
+  return float2v{red[0][0] + red[0][1] + red[0][2] + red[0][3], red[1][0] + red[1][1] + red[1][2] + red[1][3]};
 }
 
 // ---- residual + LayerNorm -------------------------------------------------------------------
@@ -83,63 +102,79 @@ __global__ __launch_bounds__(NTR) void esmc_ln_kernel(EsmcLnArgs p) {
 }
 
 // ---- QK-LayerNorm + RoPE, head-major outputs ---------------------------------------------------
-// Thread -> rotation pairs (e, e + hd/2) of one head: pair index u = tid + 256 j,
-// head = u / (hd/2), i = u % (hd/2). hd = 64.
+// Thread -> chunks of 8 rotation pairs: chunk u < D/16 of q, else of k (u' = u mod D/16);
+// pairs (e, e + 32) of head u' / 4 at e = 8 (u' % 4) .. + 7, so a chunk is two 16-byte
+// loads and two 16-byte stores. The LayerNorm statistics of q and k are reduced together.
 __global__ __launch_bounds__(NTR) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
-  __shared__ float red[4];
-  constexpr int HD = 64, HALF = 32, MAXP = 8;  // D <= 8 * 256 * 2
-  const int row = blockIdx.x, D = p.H * HD;
+  __shared__ float red[2][4];
+  constexpr int HD = 64, HALF = 32, MAXC = 2;  // 2 * D / 16 <= MAXC * NTR for D <= 4096
+  const int row = blockIdx.x, D = p.H * HD, nq = D / 16;
   const int b = row / p.L, l = row - b * p.L;
   const half_t* src = p.qkv + (size_t)row * 3 * D;
-  const int npairs = D / 2;
-  // rotation angles of this thread's pairs: l * base^(-2i/hd)
-  float cs[MAXP], sn[MAXP];
+  float a[MAXC][8], c[MAXC][8], sq = 0.f, sk = 0.f;
 #pragma unroll
-  for (int j = 0; j < MAXP; j++) {
+  for (int j = 0; j < MAXC; j++) {
     const int u = threadIdx.x + NTR * j;
-    const int i = u % HALF;
-    const float ang = (float)l * exp2f(-(float)(2 * i) / HD * p.log2_base);
-    sincosf(ang, &sn[j], &cs[j]);
+#pragma unroll
+    for (int e = 0; e < 8; e++) a[j][e] = c[j][e] = 0.f;
+    if (u < 2 * nq) {
+      const int which = u >= nq, uu = u - which * nq;
+      const half_t* v = src + which * D + (uu >> 2) * HD + 8 * (uu & 3);
+      const half8 x1 = ld16(v), x2 = ld16(v + HALF);
+      float t = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        a[j][e] = (float)x1[e];
+        c[j][e] = (float)x2[e];
+        t += a[j][e] + c[j][e];
+      }
+      sq += which ? 0.f : t;
+      sk += which ? t : 0.f;
+    }
   }
+  float2v sum = wg_sum2(sq, sk, red);
+  const float mq = sum[0] / D, mk = sum[1] / D;
+  sq = sk = 0.f;
 #pragma unroll
-  for (int which = 0; which < 2; which++) {  // 0: q, 1: k
-    const half_t* v = src + which * D;
-    const float* w = which ? p.k_ln : p.q_ln;
-    half_t* dst = which ? p.k : p.q;
-    float a[MAXP], c[MAXP], s = 0.f;
+  for (int j = 0; j < MAXC; j++) {
+    const int u = threadIdx.x + NTR * j;
+    if (u < 2 * nq) {
+      const float mean = u >= nq ? mk : mq;
+      float t = 0.f;
 #pragma unroll
-    for (int j = 0; j < MAXP; j++) {
-      const int u = threadIdx.x + NTR * j;
-      a[j] = c[j] = 0.f;
-      if (u < npairs) {
-        const int e = (u / HALF) * HD + (u % HALF);
-        a[j] = (float)v[e];
-        c[j] = (float)v[e + HALF];
-        s += a[j] + c[j];
+      for (int e = 0; e < 8; e++) {
+        a[j][e] -= mean;
+        c[j][e] -= mean;
+        t += a[j][e] * a[j][e] + c[j][e] * c[j][e];
       }
+      sq += u >= nq ? 0.f : t;
+      sk += u >= nq ? t : 0.f;
     }
-    const float mean = wg_sum(s, red) / D;
-    float q = 0.f;
+  }
+  sum = wg_sum2(sq, sk, red);
+  const float rq = rsqrtf(sum[0] / D + p.eps), rk = rsqrtf(sum[1] / D + p.eps);
 #pragma unroll
-    for (int j = 0; j < MAXP; j++) {
-      const int u = threadIdx.x + NTR * j;
-      if (u < npairs) {
-        a[j] -= mean;
-        c[j] -= mean;
-        q += a[j] * a[j] + c[j] * c[j];
-      }
-    }
-    const float rstd = rsqrtf(wg_sum(q, red) / D + p.eps);
+  for (int j = 0; j < MAXC; j++) {
+    const int u = threadIdx.x + NTR * j;
+    if (u < 2 * nq) {
+      const int which = u >= nq, uu = u - which * nq, hh = uu >> 2, i0 = 8 * (uu & 3);
+      const float* w = (which ? p.k_ln : p.q_ln) + hh * HD;
+      const float rstd = which ? rk : rq;
+      half8 o1, o2;
 #pragma unroll
-    for (int j = 0; j < MAXP; j++) {
-      const int u = threadIdx.x + NTR * j;
-      if (u < npairs) {
-        const int hh = u / HALF, i = u % HALF, e = hh * HD + i;
-        const float x1 = a[j] * rstd * w[e], x2 = c[j] * rstd * w[e + HALF];
-        half_t* o = dst + (((size_t)b * p.H + hh) * p.L + l) * HD;
-        o[i] = (half_t)(x1 * cs[j] - x2 * sn[j]);
-        o[i + HALF] = (half_t)(x2 * cs[j] + x1 * sn[j]);
+      for (int e = 0; e < 8; e++) {
+        const int i = i0 + e;
+        // rotation angle of pair i: l * base^(-2i/hd)
+        const float ang = (float)l * exp2f(-(float)(2 * i) / HD * p.log2_base);
+        float sn, cs;
+        sincosf(ang, &sn, &cs);
+        const float x1 = a[j][e] * rstd * w[i], x2 = c[j][e] * rstd * w[i + HALF];
+        o1[e] = (half_t)(x1 * cs - x2 * sn);
+        o2[e] = (half_t)(x2 * cs + x1 * sn);
       }
+      half_t* o = (which ? p.k : p.q) + (((size_t)b * p.H + hh) * p.L + l) * HD + i0;
+      st16(o, o1);
+      st16(o + HALF, o2);
     }
   }
   // v: copy to head-major, 8 halfs per thread
@@ -150,127 +185,185 @@ __global__ __launch_bounds__(NTR) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
 }
 
 // ---- attention ---------------------------------------------------------------------------------
-// One workgroup = 4 waves = 128 queries of one (batch, head); each wave 32 queries.
-// S^T[key][query] = K Q^T (A = K rows from LDS, B = the wave's Q fragments), so a lane
-// holds one query's scores: the softmax reductions are over registers plus one exchange
-// between the two lane halves. Rows 0-7 (and 8-15) of a 32-key block hold keys
-// {4h..4h+3, 8+4h..8+4h+3} (+16): a B fragment of O^T = V^T P^T with that k order, so P
-// goes from accumulator to operand directly; V^T's fragments are read in the same order.
-template <int NKB>
-__global__ __launch_bounds__(256, 1) void esmc_attention_kernel(EsmcAttnArgs p) {
-  constexpr int HD = 64, LP = 32 * NKB;           // keys padded to whole blocks
-  constexpr int KSTR = HD + 8;                     // K rows in LDS (halfs): 144 B, conflict-free
-  constexpr int VSTR = LP + 8;                     // V^T rows in LDS (halfs)
-  __shared__ __align__(16) half_t k_s[LP * KSTR];
-  __shared__ __align__(16) half_t vt_s[HD * VSTR];
-  __shared__ int sid_s[LP];
+// One workgroup = 4 waves = 32 queries of one (batch, head). Wave w takes keys
+// [KW w, KW (w + 1)) (KW = LP / 4): it streams its K and V rows into a private LDS region
+// with buffer loads that write LDS directly, computes S^T = K Q^T for its keys and a
+// softmax partial in fp32 (row max m_w, sum l_w, O_w = P V), and the four partials merge
+// through LDS: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w, M = max_w m_w.
+// S^T[key][query] (A = K rows, B = the Q fragments) keeps one query's scores in a lane, so
+// the softmax reductions are over registers plus one exchange between the two lane
+// halves. Rows 0-7 (and 8-15) of a 32-key block hold keys {4h..4h+3, 8+4h..8+4h+3} (+16):
+// a B fragment of O^T = V^T P^T with that k order, so P goes from accumulator to operand
+// directly; V^T's A fragments are read from row-major V with ds_read_b64_tr_b16 (4 keys
+// of one d per read). LDS key rows are 128 bytes, unpadded (a load writes 64 lanes x 16 B
+// to consecutive bytes), with their 16-byte pieces XOR-swizzled: piece p of K row n at
+// p ^ ((n >> 1) & 7), so the fragment reads of 16 rows cover the 64 banks once; piece p of
+// V row n at p ^ (4 ((n >> 1) & 1)), so the 4 rows x 64 bytes of a transposing read pass do.
+typedef short v4s __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 of V rows (128 bytes, pieces at p ^ (4 ((n >> 1) & 1))): lane j of a
+// 16-lane group names key row k0 + j / 4, d = n0 + 4 (j % 4) .. + 3; lane i receives
+// V[k0 + e][n0 + i % 16] for e = 0..3.
+DEV half4 tr_read_v(const char* vs, int k0, int n0, int lane) {
+  const int j = lane & 15, n = k0 + (j >> 2), d = n0 + 4 * (j & 3);
+  const char* ptr = vs + n * 128 + 16 * ((d >> 3) ^ (((n >> 1) & 1) << 2)) + 2 * (d & 7);
+  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(__attribute__((address_space(3))) const char*)ptr);
+  return __builtin_bit_cast(half4, v);
+}
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+template <int NKB>
+__global__ __launch_bounds__(256, NKB <= 8 ? 2 : 1) void esmc_attention_kernel(EsmcAttnArgs p) {
+  constexpr int HD = 64, LP = 32 * NKB, KW = LP / 4, KB = KW / 32;  // keys and key blocks per wave
+  static_assert(KW % 64 == 0, "whole 64-lane loads of key ids");
+  __shared__ __align__(16) char kv_s[4][2 * KW * 128];  // per wave: K rows, then V rows
+  __shared__ __align__(16) int sid_s[4][KW];
+  __shared__ float ml_s[4][2][32];                       // per wave: m and l of each query
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 31, h = lane >> 5;
   const int L = p.L;
-  const int bh = blockIdx.y, b = bh / p.H;
-  const int q0 = blockIdx.x * 128 + wave * 32;
-  const half_t* Q = p.q + (size_t)bh * L * HD;
-  const half_t* K = p.k + (size_t)bh * L * HD;
-  const half_t* V = p.v + (size_t)bh * L * HD;
+  // XCD-aware order: the query blocks of one (batch, head) are neighbours, so they run on
+  // one XCD and fetch that head's K and V into one L2.
+  const int nqb = (p.L + 31) / 32, t = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = t / nqb, b = bh / p.H;
+  const int q0 = (t - bh * nqb) * 32, key0 = KW * wave;
+  const bool live = key0 < L;  // wave-uniform: a wave past the last key only merges
+  const bool has_sid = p.sid != nullptr;
+  char* ks = kv_s[wave];
+  char* vs = kv_s[wave] + KW * 128;
 
-  // K -> LDS rows, V -> LDS transposed; keys past L are zero. Every load is issued before
-  // the first LDS write (a rolled loop waited on each iteration's loads in turn).
-  constexpr int NCH = LP * (HD / 8) / 256;  // 16-byte chunks of K (and of V) per thread
-  static_assert(LP * (HD / 8) % 256 == 0, "whole chunks per thread");
-  const rsrc_t rk = make_rsrc(K), rv = make_rsrc(V);
-  half8 kv[NCH], vv[NCH];
+  // K, V rows and key ids of this wave's keys; keys past L load zeros (and are masked).
+  if (live) {
+    const rsrc_t rk = make_rsrc_n(p.k + (size_t)bh * L * HD, (uint32_t)L * HD * 2u);
+    const rsrc_t rv = make_rsrc_n(p.v + (size_t)bh * L * HD, (uint32_t)L * HD * 2u);
 #pragma unroll
-  for (int i = 0; i < NCH; i++) {
-    const int c = tid + 256 * i, key = c / (HD / 8), d0 = 8 * (c % (HD / 8));
-    const uint32_t off = key < L ? (uint32_t)(key * HD + d0) * 2u : kOOB;
-    kv[i] = bload16(rk, off);
-    vv[i] = bload16(rv, off);
+    for (int i = 0; i < KW / 8; i++) {
+      const int n = 8 * i + (lane >> 3), lp = lane & 7;  // row n of this wave's keys, LDS piece lp
+      const uint32_t row = (uint32_t)(key0 + n) * 128u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(ks + 1024 * i), 16,
+                                               (int)(row + 16u * (lp ^ ((n >> 1) & 7))), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(vs + 1024 * i), 16,
+                                               (int)(row + 16u * (lp ^ (((n >> 1) & 1) << 2))), 0, 0, 0);
+    }
+    if (has_sid) {
+      const rsrc_t rs = make_rsrc_n(p.sid + (size_t)b * L, (uint32_t)L * 4u);
+#pragma unroll
+      for (int i = 0; i < KW / 64; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(&sid_s[wave][64 * i]),
+                                                 4, (int)((uint32_t)(key0 + 64 * i + lane) * 4u), 0, 0, 0);
+    }
   }
-#pragma unroll
-  for (int i = 0; i < NCH; i++) {
-    const int c = tid + 256 * i, key = c / (HD / 8), d0 = 8 * (c % (HD / 8));
-    st16(&k_s[key * KSTR + d0], kv[i]);
-#pragma unroll
-    for (int e = 0; e < 8; e++) vt_s[(d0 + e) * VSTR + key] = vv[i][e];
-  }
-  for (int key = tid; key < LP; key += 256) sid_s[key] = key < L ? (p.sid ? p.sid[(size_t)b * L + key] : 0) : -2;
-  __syncthreads();
-  if (q0 >= L) return;  // a wave past the last query (no later barrier)
 
-  // this wave's Q fragments (B operand: column = query, k = 16 ks + 8 h + e)
+  // Q fragments (B operand: column = query, k = 16 ks + 8 h + e)
   const int qrow = q0 + r;
   half8 qf[HD / 16];
+  const rsrc_t rq = make_rsrc_n(p.q + (size_t)bh * L * HD, (uint32_t)L * HD * 2u);
 #pragma unroll
-  for (int ks = 0; ks < HD / 16; ks++) qf[ks] = qrow < L ? ld16(Q + (size_t)qrow * HD + 16 * ks + 8 * h) : zero_half8();
-  const int qsid = qrow < L ? (p.sid ? p.sid[(size_t)b * L + qrow] : 0) : -3;
+  for (int ks4 = 0; ks4 < HD / 16; ks4++) qf[ks4] = bload16(rq, qrow < L ? (uint32_t)(qrow * HD + 16 * ks4 + 8 * h) * 2u : kOOB);
+  const int qsid = has_sid && qrow < L ? p.sid[(size_t)b * L + qrow] : 0;
+  __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0): this wave's LDS rows and Q are in
+  __asm__ volatile("" ::: "memory");
 
-  const int nkb = (L + 31) / 32;
-  f32x16 s[NKB];
+  f32x16 s[KB];
   float mx = -INFINITY;
+  if (live) {
 #pragma unroll
-  for (int kb = 0; kb < NKB; kb++) {
-    if (kb < nkb) {
+    for (int kb = 0; kb < KB; kb++) {
 #pragma unroll
       for (int i = 0; i < 16; i++) s[kb][i] = 0.f;
+      const int n = 32 * kb + r;
 #pragma unroll
-      for (int ks = 0; ks < HD / 16; ks++)
-        s[kb] = mfma32(ld16(&k_s[(32 * kb + r) * KSTR + 16 * ks + 8 * h]), qf[ks], s[kb]);
+      for (int ks4 = 0; ks4 < HD / 16; ks4++) {
+        const half8 kf = *reinterpret_cast<const half8*>(ks + n * 128 + 16 * ((2 * ks4 + h) ^ ((n >> 1) & 7)));
+        s[kb] = mfma32(kf, qf[ks4], s[kb]);
+      }
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const int key = 32 * kb + acc_row32(i, lane);
-        const bool ok = key < L && sid_s[key] == qsid;
-        s[kb][i] = ok ? s[kb][i] * p.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, s[kb][i]);
+      for (int i4 = 0; i4 < 4; i4++) {
+        const int kl = 32 * kb + acc_row32(4 * i4, lane);  // 4 consecutive keys of this wave
+        int4 sid4 = {0, 0, 0, 0};
+        if (has_sid) sid4 = *reinterpret_cast<const int4*>(&sid_s[wave][kl]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int i = 4 * i4 + e;
+          const bool ok = key0 + kl + e < L && sid4[e] == qsid;
+          s[kb][i] = ok ? s[kb][i] * p.scale_log2 : -INFINITY;
+          mx = fmaxf(mx, s[kb][i]);
+        }
       }
     }
   }
   mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mref = mx == -INFINITY ? 0.f : mx;  // no key of this wave is visible to the query
   float sum = 0.f;
-  half8 pf[2 * NKB];
-#pragma unroll
-  for (int kb = 0; kb < NKB; kb++) {
-    if (kb < nkb) {
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const float e = exp2f(s[kb][i] - mx);
-        sum += e;
-        pf[2 * kb + (i >> 3)][i & 7] = (half_t)e;
-      }
-    }
-  }
-  sum += __shfl_xor(sum, 32);
-
-  // O^T[d][query] = sum over keys of V^T[d][key] P[key][query]
+  half8 pf[2 * KB];
   f32x16 o[HD / 32];
 #pragma unroll
   for (int db = 0; db < HD / 32; db++)
 #pragma unroll
     for (int i = 0; i < 16; i++) o[db][i] = 0.f;
+  if (live) {
 #pragma unroll
-  for (int j = 0; j < 2 * NKB; j++) {
-    if (j < 2 * nkb) {
-      const int k0 = 16 * j + 4 * h;
+    for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float e = exp2f(s[kb][i] - mref);
+        sum += e;
+        pf[2 * kb + (i >> 3)][i & 7] = (half_t)e;
+      }
+    // O^T[d][query] = sum over this wave's keys of V^T[d][key] P[key][query]
+    const int n0q = 16 * ((lane >> 4) & 1);  // d offset of this lane's 16-lane group
+#pragma unroll
+    for (int j = 0; j < 2 * KB; j++) {
 #pragma unroll
       for (int db = 0; db < HD / 32; db++) {
-        const half_t* vr = &vt_s[(32 * db + r) * VSTR];
-        const half4 lo = *reinterpret_cast<const half4*>(vr + k0);
-        const half4 hi = *reinterpret_cast<const half4*>(vr + k0 + 8);
+        const half4 lo = tr_read_v(vs, 16 * j + 4 * h, 32 * db + n0q, lane);
+        const half4 hi = tr_read_v(vs, 16 * j + 8 + 4 * h, 32 * db + n0q, lane);
         o[db] = mfma32(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pf[j], o[db]);
       }
     }
   }
+  sum += __shfl_xor(sum, 32);
+
+  // Partials -> LDS: m, l per query; O_w in accumulator order over this wave's K rows
+  // (8 quads x 64 lanes x 16 B = 8 KB, no longer read by anyone).
+  if (h == 0) {
+    ml_s[wave][0][r] = mx;
+    ml_s[wave][1][r] = sum;
+  }
+  f32x4* ow = reinterpret_cast<f32x4*>(ks);
+#pragma unroll
+  for (int db = 0; db < HD / 32; db++)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; r4++)
+      ow[(4 * db + r4) * 64 + lane] = f32x4{o[db][4 * r4], o[db][4 * r4 + 1], o[db][4 * r4 + 2], o[db][4 * r4 + 3]};
+  __syncthreads();
+
+  // Wave w finishes quads 2w, 2w + 1: d = 32 db + acc_row32(4 r4, lane) .. + 3 of query r.
   if (qrow < L) {
-    const float inv = 1.0f / sum;
+    float m4[4], M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      m4[w] = ml_s[w][0][r];
+      M = fmaxf(M, m4[w]);
+    }
+    float den = 0.f, sc[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      sc[w] = exp2f(m4[w] - M);  // 0 for a wave that saw no visible key
+      den += sc[w] * ml_s[w][1][r];
+    }
+    const float inv = 1.0f / den;
     half_t* dst = p.o + ((size_t)b * L + qrow) * (p.H * HD) + (bh - b * p.H) * HD;
 #pragma unroll
-    for (int db = 0; db < HD / 32; db++)
+    for (int u = 0; u < 2; u++) {
+      const int qd = 2 * wave + u, db = qd >> 2, r4 = qd & 3;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r4 = 0; r4 < 4; r4++) {
-        const int d = 32 * db + acc_row32(4 * r4, lane);
-        *reinterpret_cast<half4*>(dst + d) = half4{(half_t)(o[db][4 * r4] * inv), (half_t)(o[db][4 * r4 + 1] * inv),
-                                                   (half_t)(o[db][4 * r4 + 2] * inv), (half_t)(o[db][4 * r4 + 3] * inv)};
-      }
+      for (int w = 0; w < 4; w++) acc += sc[w] * reinterpret_cast<const f32x4*>(kv_s[w])[qd * 64 + lane];
+      const int d = 32 * db + acc_row32(4 * r4, lane);
+      *reinterpret_cast<half4*>(dst + d) =
+          half4{(half_t)(acc[0] * inv), (half_t)(acc[1] * inv), (half_t)(acc[2] * inv), (half_t)(acc[3] * inv)};
+    }
   }
 }
 
@@ -303,7 +396,7 @@ hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_esmc_attention(const EsmcAttnArgs& a, hipStream_t s) {
-  const dim3 grid((a.L + 127) / 128, a.B * a.H);
+  const dim3 grid(((a.L + 31) / 32) * a.B * a.H);
   if (a.L <= 256)
     hipLaunchKernelGGL(esmc_attention_kernel<8>, grid, dim3(256), 0, s, a);
   else

@@ -118,6 +118,26 @@ def test_block(gpu_lib, pkg, D, F_, H, L, masked):
     assert err <= 1e-2 * float(upd.pow(2).mean().sqrt()), err
 
 
+def test_block_graph_replay(gpu_lib, pkg):
+    """The block captured as one HIP graph: every replay equals the eager result bit for bit,
+    with eager launches of the block between the replays."""
+    D, F_, H, L = 256, 384, 4, 37
+    blk = _module_block(pkg, _weights(D, F_, seed=3), H)
+    x = (2 * torch.randn(1, L, D, generator=_gen(7))).to(DEV)
+    ref = blk(x, None, res_scale=1.5)  # also allocates the layers' workspaces outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = blk(x, None, res_scale=1.5)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), i
+        other = blk(x * (i + 2), None, res_scale=1.5)  # eager work between the replays
+        torch.cuda.synchronize()
+        assert not torch.equal(other, ref)
+
+
 def test_hip_esmc_hidden_states_and_cache(gpu_lib, pkg, tmp_path):
     D, F_, H, n = 256, 384, 4, 3
     ps = [_weights(D, F_, seed=10 + i) for i in range(n)]
