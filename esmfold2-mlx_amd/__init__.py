@@ -12,16 +12,20 @@ Modules:
   recycle          -- ParcaeLoop (the 6B recycling loop) and its distogram exit signal
   var_hip_trimul   -- the reference-style variant plugin for the TMUs: apply(model)
   var_hip_trunk    -- the variant plugin replacing the whole folding trunk: apply(model)
+  var_6b_hip_trunks -- the variant plugin replacing all four trunk stacks of the 6B model
+  variants         -- apply_variants(model, names): the plugins by name, in order
   workloads        -- seeded synthetic inputs of the benchmark configurations
 """
 
 from . import build, capi  # noqa: F401
 
-__all__ = ["build", "capi", "kernels", "trimul", "q8", "esmc", "trunk", "recycle", "var_hip_trimul", "var_hip_trunk", "workloads"]
+__all__ = ["build", "capi", "kernels", "trimul", "q8", "esmc", "trunk", "recycle", "var_hip_trimul", "var_hip_trunk",
+           "var_6b_hip_trunks", "variants", "workloads"]
 
 
 def __getattr__(name):
-    if name in ("kernels", "trimul", "q8", "esmc", "trunk", "recycle", "var_hip_trimul", "var_hip_trunk", "workloads"):
+    if name in ("kernels", "trimul", "q8", "esmc", "trunk", "recycle", "var_hip_trimul", "var_hip_trunk",
+                "var_6b_hip_trunks", "variants", "workloads"):
         import importlib
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)

@@ -82,3 +82,21 @@ class Model(nn.Module):
     def __init__(self, blocks):
         super().__init__()
         self.folding_trunk = FoldingTrunk(blocks)
+
+
+class ConfidenceHead(nn.Module):
+    def __init__(self, blocks):
+        super().__init__()
+        self.folding_trunk = FoldingTrunk(blocks)
+
+
+class Model6B(nn.Module):
+    """The 6B release model's four trunk stacks (var_6b_mlx_trunks16k.py:29-32); ``lm`` may be
+    None (no lm_encoder)."""
+
+    def __init__(self, main, lm, coda, conf):
+        super().__init__()
+        self.folding_trunk = FoldingTrunk(main)
+        self.lm_encoder = FoldingTrunk(lm) if lm is not None else None
+        self.parcae_coda = FoldingTrunk(coda)
+        self.confidence_head = ConfidenceHead(conf)

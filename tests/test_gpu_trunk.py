@@ -99,6 +99,35 @@ def test_var_hip_trunk_plugin_swiglu(gpu_lib, pkg):
     _check(out, z, ref, bar=3e-2, norm_bar=1e-2)
 
 
+@pytest.mark.parametrize("with_lm", [True, False])
+def test_var_6b_hip_trunks_plugin(gpu_lib, pkg, with_lm):
+    """All four trunk stacks of a 6B-shaped model, through apply_variants by name; a stack
+    already replaced by an earlier variant is kept."""
+    L = 18
+    stacks = {name: pkg.workloads.block_stack(L, n_blocks=n, H=256, seed=20 + k)
+              for k, (name, n) in enumerate((("main", 2), ("lm", 1), ("coda", 1), ("conf", 1)))}
+    g = torch.Generator().manual_seed(11)
+    for _, blocks in stacks.values():  # SwiGLU transitions, as the reference's trunk modules have
+        for _, _, pt in blocks:
+            pt.w2 = torch.randn(256, 128, generator=g) * 128 ** -0.5
+    model = ref_modules.Model6B(stacks["main"][1], stacks["lm"][1] if with_lm else None, stacks["coda"][1],
+                                stacks["conf"][1])
+    pkg.variants.apply_variants(model, ["hip_trunk", "", "6b_hip_trunks"])
+    main = model.folding_trunk
+    pkg.variants.apply_variants(model, ["6b_hip_trunks"])
+    assert model.folding_trunk is main
+    got = {"main": model.folding_trunk, "coda": model.parcae_coda, "conf": model.confidence_head.folding_trunk}
+    if with_lm:
+        got["lm"] = model.lm_encoder
+    else:
+        assert model.lm_encoder is None
+    for name, trunk in got.items():
+        assert isinstance(trunk, pkg.trunk.PairTrunk), name
+        z, blocks = stacks[name]
+        ref = otr.stack_forward(z.double(), None, _oracle_blocks(blocks), 1, store=torch.float16)
+        _check(trunk(z.to(DEV).float()), z, ref, bar=3e-2, norm_bar=1e-2)
+
+
 def test_var_hip_trimul_plugin(gpu_lib, pkg):
     z, mask, po, pi = pkg.workloads.pair_inputs(30, seed=2, pad_from=25)
     _, blocks = pkg.workloads.block_stack(4, n_blocks=1, H=256)
