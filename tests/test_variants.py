@@ -31,3 +31,20 @@ def test_6b_plugin_keeps_replaced_stacks_and_a_missing_lm_encoder(pkg):
     pkg.var_6b_hip_trunks.apply(model)
     assert (model.folding_trunk, model.parcae_coda, model.confidence_head.folding_trunk) == before
     assert model.lm_encoder is None
+
+
+def test_missing_dependency_inside_a_variant_propagates(pkg, monkeypatch):
+    """Only a missing var_<name> module is an unknown variant; a module missing inside an
+    existing variant's import is reported as itself (variants.py:79-83)."""
+    import importlib
+
+    real = importlib.import_module
+
+    def fake(name, *a, **k):
+        if name.endswith(".var_hip_trunk"):
+            raise ModuleNotFoundError("No module named 'somedep'", name="somedep")
+        return real(name, *a, **k)
+
+    monkeypatch.setattr(importlib, "import_module", fake)
+    with pytest.raises(ModuleNotFoundError, match="somedep"):
+        pkg.variants.apply_variants(torch.nn.Module(), ["hip_trunk"])
