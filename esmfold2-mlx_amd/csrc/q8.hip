@@ -249,7 +249,6 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     for (int w = 1; w < NWQ; w++) v += red[w][blk][r4][lane];
     return v;
   };
-  const int tile_id = nt * p.mtiles + mt;
   if (p.splits == 1) {
     for (int blk = wave; blk < NBLK; blk += NWQ) {
       const int mb = blk / NBQ, nb = blk - mb * NBQ;

@@ -164,19 +164,27 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
 }
 
 // ---- quantile of |x - y| ----------------------------------------------------------------------
-// One workgroup. Radix selection on the bit patterns of the non-negative values (their
-// order is the value order): 3 passes of 11, 11 and 10 bits, each a histogram of the
+// One workgroup of QT threads. Radix selection on the bit patterns of the non-negative values
+// (their order is the value order): 3 passes of 11, 11 and 10 bits, each a histogram of the
 // candidates still matching the selected high bits, for the two ranks that bracket the
 // quantile at once; then linear interpolation between the two order statistics (the
-// definition of torch.quantile).
-__global__ __launch_bounds__(1024) void abs_diff_quantile_kernel(const float* __restrict__ x,
-                                                                 const float* __restrict__ y, size_t n, float q,
-                                                                 float* __restrict__ out) {
-  constexpr int NBIN = 2048;
+// definition of torch.quantile). While both ranks share their selected high bits (always in
+// the first pass, and in most later ones since the ranks are adjacent) one histogram serves
+// both. Up to QT * QC values the patterns stay in registers after the first pass (thread tid
+// holds values tid + QT j), so only one pass reads memory; beyond that every pass scans x and
+// y in chunks of QT * QU values. Loads go through range-checked buffer descriptors with no
+// branch around them, so a thread's loads are in flight together.
+constexpr int QT = 1024;
+__global__ __launch_bounds__(QT) void abs_diff_quantile_kernel(const float* __restrict__ x,
+                                                               const float* __restrict__ y, size_t n, float q,
+                                                               float* __restrict__ out) {
+  constexpr int NBIN = 2048, BPT = NBIN / QT, NWV = QT / 64, QU = 8, QC = 56;
+  constexpr uint32_t kNone = 0xffffffffu;  // an index past n: no prefix of a |value| matches it
   __shared__ uint32_t hist[2][NBIN];
   __shared__ uint32_t sel[2];
+  __shared__ uint32_t wsum[2][NWV];
   __shared__ unsigned long long rank_s[2];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const double pos = (double)q * (double)(n - 1);
   const unsigned long long lo = (unsigned long long)pos;
   const unsigned long long hi = lo + 1 < n ? lo + 1 : lo;
@@ -185,46 +193,114 @@ __global__ __launch_bounds__(1024) void abs_diff_quantile_kernel(const float* __
     rank_s[0] = lo;
     rank_s[1] = hi;
   }
+  // Values [c0, c0 + cnt): x and y descriptors of exactly that range (y absent: range 0,
+  // which loads zeros).
+  auto chunk = [&](size_t c0, size_t cnt, rsrc_t& rx, rsrc_t& ry) {
+    rx = make_rsrc_n(x + c0, (uint32_t)(cnt * 4));
+    ry = make_rsrc_n(y ? y + c0 : x, y ? (uint32_t)(cnt * 4) : 0u);
+  };
+  // value tid + QT j: the per-thread part in the vector offset, the per-load part in the
+  // scalar offset (no address register per load)
+  auto ld = [&](const rsrc_t& r, int j) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, tid * 4, QT * 4 * j, 0);
+  };
+  // |x - y| as a bit pattern; an OR rather than a select, which would let the compiler sink
+  // the loads under a branch
+  auto pattern = [&](uint32_t xb, uint32_t yb, uint32_t i, size_t cnt) {
+    return __float_as_uint(fabsf(__uint_as_float(xb) - __uint_as_float(yb))) | (i < cnt ? 0u : kNone);
+  };
+  const bool cached = n <= (size_t)QT * QC;
+  uint32_t uc[QC];
   uint32_t prefix[2] = {0u, 0u}, mask = 0u;
   const int shifts[3] = {21, 10, 0}, widths[3] = {11, 11, 10};
+#pragma unroll
   for (int ps = 0; ps < 3; ps++) {
     const int sh = shifts[ps];
     const uint32_t bmask = (1u << widths[ps]) - 1u;
-    for (int k = tid; k < 2 * NBIN; k += 1024) (&hist[0][0])[k] = 0u;
+    const bool shared = prefix[0] == prefix[1];  // block-uniform
+    auto count = [&](uint32_t u) {
+      const uint32_t bin = (u >> sh) & bmask;
+      if ((u & mask) == prefix[0] && u != kNone) atomicAdd(&hist[0][bin], 1u);
+      if (!shared && (u & mask) == prefix[1] && u != kNone) atomicAdd(&hist[1][bin], 1u);
+    };
+    for (int k = tid; k < 2 * NBIN; k += QT) (&hist[0][0])[k] = 0u;
     __syncthreads();
-    for (size_t idx = tid; idx < n; idx += 1024) {
-      const float v = y ? fabsf(x[idx] - y[idx]) : fabsf(x[idx]);
-      const uint32_t u = __float_as_uint(v);
+    if (cached) {
+      if (ps == 0) {
+        // all of x in flight, then y in groups of 8
+        rsrc_t rx, ry;
+        chunk(0, n, rx, ry);
 #pragma unroll
-      for (int t = 0; t < 2; t++)
-        if ((u & mask) == prefix[t]) atomicAdd(&hist[t][(u >> sh) & bmask], 1u);
+        for (int j = 0; j < QC; j++) uc[j] = ld(rx, j);
+#pragma unroll
+        for (int g = 0; g < QC / 8; g++) {
+          uint32_t yb[8];
+#pragma unroll
+          for (int j = 0; j < 8; j++) yb[j] = ld(ry, 8 * g + j);
+#pragma unroll
+          for (int j = 0; j < 8; j++)
+            uc[8 * g + j] = pattern(uc[8 * g + j], yb[j], (uint32_t)(tid + QT * (8 * g + j)), n);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < QC; j++) count(uc[j]);
+    } else {
+      for (size_t c0 = 0; c0 < n; c0 += (size_t)QT * QU) {
+        const size_t cnt = n - c0 < (size_t)QT * QU ? n - c0 : (size_t)QT * QU;
+        rsrc_t rx, ry;
+        chunk(c0, cnt, rx, ry);
+        uint32_t xb[QU], yb[QU];
+#pragma unroll
+        for (int j = 0; j < QU; j++) {
+          xb[j] = ld(rx, j);
+          yb[j] = ld(ry, j);
+        }
+#pragma unroll
+        for (int j = 0; j < QU; j++) count(pattern(xb[j], yb[j], (uint32_t)(tid + QT * j), cnt));
+      }
     }
     __syncthreads();
-    if (tid < 64) {  // wave 0: find each rank's bin
+    // Each rank's bin: thread tid owns bins BPT tid .. BPT tid + BPT - 1; an exclusive scan of
+    // the bin counts over the workgroup (64-lane scans, then the wave totals) gives each thread
+    // the number of candidates below its bins, and the thread whose bins hold the rank records
+    // the bin and the rank within it.
+    {
+      unsigned long long rk[2];
+      uint32_t cb[2][BPT], c[2], inc[2];
 #pragma unroll
       for (int t = 0; t < 2; t++) {
-        uint32_t c = 0;
-        for (int k = 0; k < 32; k++) c += hist[t][32 * tid + k];
-        uint32_t inc = c;  // inclusive prefix over the 64 lanes
-        for (int off = 1; off < 64; off <<= 1) {
-          const uint32_t o = __shfl_up(inc, off);
-          if (tid >= off) inc += o;
+        const uint32_t* ht = hist[shared ? 0 : t];
+        rk[t] = rank_s[t];
+        c[t] = 0;
+#pragma unroll
+        for (int k = 0; k < BPT; k++) {
+          cb[t][k] = ht[BPT * tid + k];
+          c[t] += cb[t][k];
         }
-        const unsigned long long rk = rank_s[t];
-        const uint32_t before = inc - c;
-        if (rk >= before && rk < inc) {  // exactly one lane
-          unsigned long long run = before;
-          int bin = 32 * tid;
-          for (int k = 0; k < 32; k++) {
-            const uint32_t hc = hist[t][32 * tid + k];
-            if (rk < run + hc) {
-              bin = 32 * tid + k;
-              break;
-            }
-            run += hc;
-          }
-          sel[t] = (uint32_t)bin;
-          rank_s[t] = rk - run;
+        inc[t] = c[t];
+      }
+      for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          const uint32_t o = __shfl_up(inc[t], off);
+          if (lane >= off) inc[t] += o;
+        }
+      }
+      if (lane == 63) {
+        wsum[0][wv] = inc[0];
+        wsum[1][wv] = inc[1];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        unsigned long long before = inc[t] - c[t];
+        for (int w = 0; w < wv; w++) before += wsum[t][w];
+        if (rk[t] >= before && rk[t] < before + c[t]) {  // exactly one thread
+          int k = 0;
+          while (k < BPT - 1 && rk[t] >= before + cb[t][k]) before += cb[t][k++];
+          sel[t] = (uint32_t)(BPT * tid + k);
+          rank_s[t] = rk[t] - before;
         }
       }
     }
@@ -256,7 +332,7 @@ hipError_t launch_expected_distance(const DistoArgs& a, int grid, hipStream_t s)
 }
 
 hipError_t launch_abs_diff_quantile(const float* x, const float* y, size_t n, float q, float* out, hipStream_t s) {
-  hipLaunchKernelGGL(abs_diff_quantile_kernel, dim3(1), dim3(1024), 0, s, x, y, n, q, out);
+  hipLaunchKernelGGL(abs_diff_quantile_kernel, dim3(1), dim3(QT), 0, s, x, y, n, q, out);
   return hipGetLastError();
 }
 
