@@ -135,12 +135,15 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
 #pragma unroll
       for (int e = 0; e < 8; e++) v[e] = (float)zq[it][e];
       ln_row128(v, g, bb, p.eps);
+      // Cells past L (zeros from the range-checked loads) enter the projection as zeros
+      // and get a zero mask, so their padded outputs [L, ld) are exactly 0 (their
+      // LayerNorm would be 0 * rsqrt(eps), NaN for eps = 0).
+      const bool cell_in = pos0 + cl < L;
       half8 o;
 #pragma unroll
-      for (int e = 0; e < 8; e++) o[e] = (half_t)v[e];
+      for (int e = 0; e < 8; e++) o[e] = cell_in ? (half_t)v[e] : (half_t)0.f;
       st16(&ns[cl * NS + ch0], o);
-      // cells past L get a zero mask so their padded outputs [L, ld) are exactly 0
-      const float mval = pos0 + cl < L ? (has_mask ? h2f(mq[it]) : 1.f) : 0.f;
+      const float mval = cell_in ? (has_mask ? h2f(mq[it]) : 1.f) : 0.f;
       if ((lane & 15) == 0) m_s[nb][cl] = mval;
     }
     __syncthreads();

@@ -81,6 +81,25 @@ def test_project_kernel(gpu_lib, pkg, L, incoming, mask_kind):
     assert torch.count_nonzero(a[..., L:]) == 0 and torch.count_nonzero(b[..., L:]) == 0, "pad columns not zero"
 
 
+@pytest.mark.parametrize("incoming", [False, True])
+def test_project_kernel_eps_zero_padding(gpu_lib, pkg, incoming):
+    """eps = 0 is accepted: the padding cells past L (zero inputs, zero variance) must still give
+    exact zeros in the pad columns, not 0 * rsqrt(0) = NaN, which the contraction would spread."""
+    L = 65
+    p = _weights(L, not incoming, random_ln=True)
+    z = _z(L, 1, L)
+    a, b = pkg.kernels.project(z.to(DEV), None, p.ln_in_w.to(DEV), p.ln_in_b.to(DEV), 0.0,
+                               p.w_bundle.half().to(DEV), incoming)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(a[..., L:]) == 0 and torch.count_nonzero(b[..., L:]) == 0
+    assert torch.isfinite(a).all() and torch.isfinite(b).all()
+    p0 = p.to(F64)
+    p0.ln_in_eps = 0.0
+    ra, rb = _oracle_project(z, None, p0, incoming)
+    _bar(a[..., :L], ra)
+    _bar(b[..., :L], rb)
+
+
 @pytest.mark.parametrize("L", [1, 8, 33, 128, 129, 238])
 def test_contract_kernel(gpu_lib, pkg, L):
     g = torch.Generator().manual_seed(L)
