@@ -241,6 +241,7 @@ int pair_transition(const esm_half* z, esm_half* out, const float* ln_w, const f
   if (C != 128) return fail(ESM_ERR_UNSUPPORTED, "pair_transition: C=%d (supported: 128)", C);
   if (w2 ? hidden != 256 : (hidden != 256 && hidden != 512))
     return fail(ESM_ERR_UNSUPPORTED, "pair_transition: H=%d (supported: ReLU 256 or 512, SwiGLU 256)", hidden);
+  if (!(eps >= 0.f)) return fail(ESM_ERR_SHAPE, "pair_transition: eps must be >= 0");
   if (B == 0 || L == 0) return ok();
   if (L > kMaxL) return fail(ESM_ERR_SHAPE, "pair_transition: L=%d exceeds %d", L, kMaxL);
   const size_t ncells = (size_t)B * L * L;
@@ -259,6 +260,7 @@ int esmc_layer_norm(const float* x, const esm_half* y, float alpha, float* x_out
                     float eps, esm_half* h, float* h_fp32, int M, int D, void* stream) {
   if (M < 0 || D <= 0) return fail(ESM_ERR_SHAPE, "esmc_layer_norm: M=%d D=%d", M, D);
   if (D % 8 != 0 || D > 8192) return fail(ESM_ERR_UNSUPPORTED, "esmc_layer_norm: D=%d (multiple of 8, <= 8192)", D);
+  if (!(eps >= 0.f)) return fail(ESM_ERR_SHAPE, "esmc_layer_norm: eps must be >= 0");
   if (M == 0) return ok();
   if (!x || !w || (!h == !h_fp32) || (y && !x_out))
     return fail(ESM_ERR_NULL, "esmc_layer_norm: NULL pointer (exactly one of h, h_fp32 is written)");
@@ -275,6 +277,7 @@ int esmc_qk_rope(const esm_half* qkv, const float* q_ln, const float* k_ln, floa
   if (head_dim != 64 || n_heads * 64 > 4096)
     return fail(ESM_ERR_UNSUPPORTED, "esmc_qk_rope: head_dim=%d heads=%d (head_dim 64, width <= 4096)", head_dim,
                 n_heads);
+  if (!(eps >= 0.f)) return fail(ESM_ERR_SHAPE, "esmc_qk_rope: eps must be >= 0");
   if (B == 0 || L == 0) return ok();
   if (!qkv || !q_ln || !k_ln || !q || !k || !v) return fail(ESM_ERR_NULL, "esmc_qk_rope: NULL pointer");
   if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || !aligned16(v))
@@ -309,6 +312,7 @@ int parcae_step(const float* z, const float* z_init, const float* refined, const
                 float eps, const float* a, const esm_half* b_mat, float* z_out, int B, int L, int C, void* stream) {
   if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "parcae_step: B=%d L=%d must be >= 0", B, L);
   if (C != 128) return fail(ESM_ERR_UNSUPPORTED, "parcae_step: C=%d (supported: 128)", C);
+  if (!(eps >= 0.f)) return fail(ESM_ERR_SHAPE, "parcae_step: eps must be >= 0");
   if (B == 0 || L == 0) return ok();
   const size_t ncells = (size_t)B * L * L;
   if (ncells * C * 4 >= (1ull << 31)) return fail(ESM_ERR_SHAPE, "parcae_step: B*L*L=%zu cells exceed 2 GB", ncells);

@@ -10,6 +10,8 @@
  * Return codes: 0 = success; a negative ESM_ERR_* value = the arguments were
  * rejected before launch (nothing ran); a positive value = a hipError_t reported
  * by the runtime. esm_last_error() gives a message for the calling thread.
+ * Every LayerNorm eps argument must be >= 0 (a negative or NaN eps is
+ * ESM_ERR_SHAPE).
  *
  * Element types: fp16 values are IEEE binary16 (passed as uint16_t bit patterns,
  * esm_half); fp32 values are float; 8-bit codes are uint8_t.

@@ -72,6 +72,13 @@ def test_rejects_null_and_bad_shapes(lib):
     assert lib.pair_transition(None, None, None, None, 1e-5, None, ctypes.c_void_p(4096), None, 1, 8, 128, 512,
                                None) == -4  # SwiGLU at H=512
     assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 0, 8, 128, 512, None) == 0
+    # a negative or NaN eps is refused by every LayerNorm entry point, before any pointer is used
+    for eps in (-1e-5, float("nan")):
+        assert lib.pair_transition(None, None, None, None, eps, None, None, None, 1, 8, 128, 512, None) == -2
+        assert lib.esmc_layer_norm(None, None, 0.0, None, None, None, eps, None, None, 4, 64, None) == -2
+        assert lib.esmc_qk_rope(None, None, None, eps, None, None, None, 1, 8, 4, 64, 10000.0, None) == -2
+        assert lib.parcae_step(*([None] * 5), eps, None, None, None, 1, 8, 128, None) == -2
+        assert "eps" in _err(lib)
     assert lib.q8_pack_scales(None, None, None, 64, 128, 64, None) == -1
     assert lib.q8_pack_scales(None, None, None, 64, 100, 64, None) == -2
     assert lib.q8_packed_scales_bytes(64, 128) == 1 * 2 * 160 * 4 and lib.q8_packed_scales_bytes(161, 64) == 2 * 160 * 4
