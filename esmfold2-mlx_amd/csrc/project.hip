@@ -135,16 +135,15 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
 #pragma unroll
       for (int e = 0; e < 8; e++) v[e] = (float)zq[it][e];
       ln_row128(v, g, bb, p.eps);
-      // Cells past L (zeros from the range-checked loads) enter the projection as zeros
-      // and get a zero mask, so their padded outputs [L, ld) are exactly 0 (their
+      // Cells past L (zeros from the range-checked loads) enter the projection as zeros,
+      // so their padded outputs [L, ld) are exactly 0 with or without a mask (their
       // LayerNorm would be 0 * rsqrt(eps), NaN for eps = 0).
       const bool cell_in = pos0 + cl < L;
       half8 o;
 #pragma unroll
       for (int e = 0; e < 8; e++) o[e] = cell_in ? (half_t)v[e] : (half_t)0.f;
       st16(&ns[cl * NS + ch0], o);
-      const float mval = cell_in ? (has_mask ? h2f(mq[it]) : 1.f) : 0.f;
-      if ((lane & 15) == 0) m_s[nb][cl] = mval;
+      if (has_mask && (lane & 15) == 0) m_s[nb][cl] = cell_in ? h2f(mq[it]) : 0.f;
     }
     __syncthreads();
 
@@ -173,10 +172,15 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
 #pragma unroll
       for (int r4 = 0; r4 < 4; r4++) {
         const int c4 = 32 * h + acc_row32(4 * r4, lane);  // first of this group's 4 cells
-        const f32x4 m4 = *reinterpret_cast<const f32x4*>(&m_s[nb][c4]);
         half4 v;
+        if (has_mask) {
+          const f32x4 m4 = *reinterpret_cast<const f32x4*>(&m_s[nb][c4]);
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = (half_t)(as[h][4 * r4 + e] * sigmoidf_fast(ag[h][4 * r4 + e]) * m4[e]);
+          for (int e = 0; e < 4; e++) v[e] = (half_t)(as[h][4 * r4 + e] * sigmoidf_fast(ag[h][4 * r4 + e]) * m4[e]);
+        } else {  // a padding cell's signal is already 0 (zero LayerNorm row)
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[e] = (half_t)(as[h][4 * r4 + e] * sigmoidf_fast(ag[h][4 * r4 + e]));
+        }
         *reinterpret_cast<half4*>(&st[st_off(lane & 31, c4)]) = v;
       }
     // The staging rows are private to the wave and a wave's LDS operations complete in
