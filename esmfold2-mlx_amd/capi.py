@@ -29,6 +29,7 @@ SIGNATURES = {
                            _int, _int, _int, _int, _vp]),
     "pair_transition": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "esmc_layer_norm": (_int, [_vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int, _int, _vp]),
+    "esmc_layer_norm_parts": (_int, [_vp, _vp, _int, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int, _int, _vp]),
     "esmc_qk_rope": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _f32, _vp]),
     "esmc_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _f32, _vp]),
     "esmc_swiglu": (_int, [_vp, _vp, _int, _int, _vp]),
@@ -38,6 +39,8 @@ SIGNATURES = {
     "q8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "q8_linear_ws": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
     "q8_linear_workspace_bytes": (_sz, [_int, _int, _int]),
+    "q8_linear_partials_bytes": (_sz, [_int, _int, _int]),
+    "q8_linear_partials": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _int, _int, _int, _int, _vp]),
     "q8_packed_scales_bytes": (_sz, [_int, _int]),
     "q8_pack_scales": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp]),
     "q8_dequant": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]),

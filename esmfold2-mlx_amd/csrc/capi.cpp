@@ -198,20 +198,34 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
                       w_emit, w_gate, out, B, L, C, c, residual, out_mask, stream);
 }
 
+// Checks shared by the q8 GEMM entry points (fn names the caller in the messages); out is
+// y (8-byte aligned) or the partials (256-byte aligned). Sets *empty for a no-op shape.
+static int q8_check(const char* fn, const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b,
+                    const void* out, unsigned out_align, int M, int K, int N, int group, bool* empty) {
+  *empty = false;
+  if (M < 0 || K < 0 || N < 0) return fail(ESM_ERR_SHAPE, "%s: M=%d K=%d N=%d must be >= 0", fn, M, K, N);
+  if (group != 64) return fail(ESM_ERR_UNSUPPORTED, "%s: group=%d (supported: 64)", fn, group);
+  if (M == 0 || N == 0) {
+    *empty = true;
+    return ok();
+  }
+  if (K == 0 || K % 64 != 0 || N % 64 != 0)
+    return fail(ESM_ERR_SHAPE, "%s: K=%d and N=%d must be positive multiples of 64", fn, K, N);
+  if (K > kQ8MaxK) return fail(ESM_ERR_SHAPE, "%s: K=%d too large (max %d)", fn, K, kQ8MaxK);
+  if ((long long)N * K >= (1LL << 31) || (long long)M * K * 2 >= (1LL << 31))
+    return fail(ESM_ERR_SHAPE, "%s: M=%d, K=%d, N=%d: x or q exceeds 2 GB", fn, M, K, N);
+  if (!x || !q || !s || !b || !out) return fail(ESM_ERR_NULL, "%s: NULL pointer", fn);
+  if (!aligned16(x) || !aligned16(q) || (reinterpret_cast<uintptr_t>(out) & (out_align - 1)) != 0 ||
+      (reinterpret_cast<uintptr_t>(s) & 1u) != 0 || (reinterpret_cast<uintptr_t>(b) & 1u) != 0)
+    return fail(ESM_ERR_ALIGN, "%s: x, q must be 16-byte aligned and the output %u-byte aligned", fn, out_align);
+  return ok();
+}
+
 int q8_linear_ws(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, const uint32_t* sb,
                  esm_half* y, int M, int K, int N, int group, void* workspace, size_t workspace_bytes, void* stream) {
-  if (M < 0 || K < 0 || N < 0) return fail(ESM_ERR_SHAPE, "q8_linear: M=%d K=%d N=%d must be >= 0", M, K, N);
-  if (group != 64) return fail(ESM_ERR_UNSUPPORTED, "q8_linear: group=%d (supported: 64)", group);
-  if (M == 0 || N == 0) return ok();
-  if (K == 0 || K % 64 != 0 || N % 64 != 0)
-    return fail(ESM_ERR_SHAPE, "q8_linear: K=%d and N=%d must be positive multiples of 64", K, N);
-  if (K > kQ8MaxK) return fail(ESM_ERR_SHAPE, "q8_linear: K=%d too large (max %d)", K, kQ8MaxK);
-  if ((long long)N * K >= (1LL << 31) || (long long)M * K * 2 >= (1LL << 31))
-    return fail(ESM_ERR_SHAPE, "q8_linear: M=%d, K=%d, N=%d: x or q exceeds 2 GB", M, K, N);
-  if (!x || !q || !s || !b || !y) return fail(ESM_ERR_NULL, "q8_linear: NULL pointer");
-  if (!aligned16(x) || !aligned16(q) || (reinterpret_cast<uintptr_t>(y) & 7u) != 0 ||
-      (reinterpret_cast<uintptr_t>(s) & 1u) != 0 || (reinterpret_cast<uintptr_t>(b) & 1u) != 0)
-    return fail(ESM_ERR_ALIGN, "q8_linear: x, q must be 16-byte aligned and y 8-byte aligned");
+  bool empty;
+  if (const int rc = q8_check("q8_linear", x, q, s, b, y, 8, M, K, N, group, &empty)) return rc;
+  if (empty) return ok();
   Q8Plan pl = q8_plan(M, K, N);
   if ((long long)pl.mtiles * pl.ntiles * pl.splits > 0x7fffffffLL)
     return fail(ESM_ERR_SHAPE, "q8_linear: M=%d N=%d too large", M, N);
@@ -227,6 +241,29 @@ int q8_linear_ws(const esm_half* x, const uint8_t* q, const esm_half* s, const e
   esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits,
                 pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear launch");
+}
+
+size_t q8_linear_partials_bytes(int M, int K, int N) {
+  if (M <= 0 || K <= 0 || N <= 0 || K % 64 != 0 || N % 64 != 0 || K > kQ8MaxK) return 0;
+  return q8_plan(M, K, N).bytes;
+}
+
+int q8_linear_partials(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, const uint32_t* sb,
+                       float* parts, size_t parts_bytes, int* splits, int M, int K, int N, int group, void* stream) {
+  bool empty;
+  if (!splits) return fail(ESM_ERR_NULL, "q8_linear_partials: NULL splits");
+  *splits = 0;
+  if (const int rc = q8_check("q8_linear_partials", x, q, s, b, parts, 256, M, K, N, group, &empty)) return rc;
+  if (empty) return ok();
+  const Q8Plan pl = q8_plan(M, K, N);
+  if ((long long)pl.mtiles * pl.ntiles * pl.splits > 0x7fffffffLL)
+    return fail(ESM_ERR_SHAPE, "q8_linear_partials: M=%d N=%d too large", M, N);
+  if (parts_bytes < pl.bytes)
+    return fail(ESM_ERR_SHAPE, "q8_linear_partials: %zu bytes for the partials, %zu needed", parts_bytes, pl.bytes);
+  if (sb && !aligned16(sb)) return fail(ESM_ERR_ALIGN, "q8_linear_partials: packed scales must be 16-byte aligned");
+  *splits = pl.splits;
+  esm::Q8Args a{H(x), q, H(s), H(b), nullptr, M, K, N, pl.mtiles, pl.ntiles, pl.splits, parts, sb};
+  return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_partials launch");
 }
 
 int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* y, int M, int K,
@@ -256,19 +293,36 @@ int pair_transition(const esm_half* z, esm_half* out, const float* ln_w, const f
   return hip_status(esm::launch_transition(a, grid, (hipStream_t)stream), "pair_transition launch");
 }
 
+// esmc_layer_norm and esmc_layer_norm_parts: y (fp16) or yp (fp32 partials of y), or neither.
+static int esmc_ln_run(const char* fn, const float* x, const esm_half* y, const float* yp, int splits, float alpha,
+                       float* x_out, const float* w, const float* b, float eps, esm_half* h, float* h_fp32, int M,
+                       int D, void* stream) {
+  if (M < 0 || D <= 0) return fail(ESM_ERR_SHAPE, "%s: M=%d D=%d", fn, M, D);
+  if (D % 8 != 0 || D > 8192) return fail(ESM_ERR_UNSUPPORTED, "%s: D=%d (multiple of 8, <= 8192)", fn, D);
+  if (!(eps >= 0.f)) return fail(ESM_ERR_SHAPE, "%s: eps must be >= 0", fn);
+  if (yp && splits < 1) return fail(ESM_ERR_SHAPE, "%s: splits=%d must be >= 1", fn, splits);
+  if (M == 0) return ok();
+  const bool add = y || yp;
+  if (!x || !w || (!h == !h_fp32) || (add && !x_out))
+    return fail(ESM_ERR_NULL, "%s: NULL pointer (exactly one of h, h_fp32 is written)", fn);
+  if (!aligned16(x) || (h && !aligned16(h)) || (h_fp32 && !aligned16(h_fp32)) || (y && !aligned16(y)) ||
+      (yp && !aligned16(yp)) || (add && !aligned16(x_out)))
+    return fail(ESM_ERR_ALIGN, "%s: x, y, x_out, h, h_fp32 must be 16-byte aligned", fn);
+  esm::EsmcLnArgs a{x, y ? H(y) : nullptr, yp, yp ? splits : 0, alpha, x_out, w, b, eps, h ? H(h) : nullptr, h_fp32,
+                    M, D};
+  return hip_status(esm::launch_esmc_ln(a, (hipStream_t)stream), "esmc_layer_norm launch");
+}
+
 int esmc_layer_norm(const float* x, const esm_half* y, float alpha, float* x_out, const float* w, const float* b,
                     float eps, esm_half* h, float* h_fp32, int M, int D, void* stream) {
-  if (M < 0 || D <= 0) return fail(ESM_ERR_SHAPE, "esmc_layer_norm: M=%d D=%d", M, D);
-  if (D % 8 != 0 || D > 8192) return fail(ESM_ERR_UNSUPPORTED, "esmc_layer_norm: D=%d (multiple of 8, <= 8192)", D);
-  if (!(eps >= 0.f)) return fail(ESM_ERR_SHAPE, "esmc_layer_norm: eps must be >= 0");
-  if (M == 0) return ok();
-  if (!x || !w || (!h == !h_fp32) || (y && !x_out))
-    return fail(ESM_ERR_NULL, "esmc_layer_norm: NULL pointer (exactly one of h, h_fp32 is written)");
-  if (!aligned16(x) || (h && !aligned16(h)) || (h_fp32 && !aligned16(h_fp32)) ||
-      (y && (!aligned16(y) || !aligned16(x_out))))
-    return fail(ESM_ERR_ALIGN, "esmc_layer_norm: x, y, x_out, h, h_fp32 must be 16-byte aligned");
-  esm::EsmcLnArgs a{x, y ? H(y) : nullptr, alpha, x_out, w, b, eps, h ? H(h) : nullptr, h_fp32, M, D};
-  return hip_status(esm::launch_esmc_ln(a, (hipStream_t)stream), "esmc_layer_norm launch");
+  return esmc_ln_run("esmc_layer_norm", x, y, nullptr, 0, alpha, x_out, w, b, eps, h, h_fp32, M, D, stream);
+}
+
+int esmc_layer_norm_parts(const float* x, const float* y_parts, int splits, float alpha, float* x_out, const float* w,
+                          const float* b, float eps, esm_half* h, float* h_fp32, int M, int D, void* stream) {
+  if (!y_parts && M > 0) return fail(ESM_ERR_NULL, "esmc_layer_norm_parts: NULL partials");
+  return esmc_ln_run("esmc_layer_norm_parts", x, nullptr, y_parts, splits, alpha, x_out, w, b, eps, h, h_fp32, M, D,
+                     stream);
 }
 
 int esmc_qk_rope(const esm_half* qkv, const float* q_ln, const float* k_ln, float eps, esm_half* q, esm_half* k,

@@ -1,6 +1,7 @@
 // Kernels of the ESMC transformer block around the 8-bit linear (mlx_esmc.py:84-102),
 // other than the q8 GEMMs themselves (q8.hip):
-//   esmc_ln        x' = x + alpha*y (fp32 residual, optional), h = LN(x') -> fp16 or fp32
+//   esmc_ln        x' = x + alpha*y (fp32 residual, optional; y fp16 or the q8 linear's
+//                  fp32 split partials), h = LN(x') -> fp16 or fp32
 //   esmc_qk_rope   QK-LayerNorm over the full width (weight only, fp32 statistics),
 //                  NeoX rotary embedding, head-major q, k, v for the attention
 //   esmc_attention softmax(q k^T * scale, same-chain mask) v, 32 queries of one head
@@ -55,6 +56,8 @@ __global__ __launch_bounds__(NTR) void esmc_ln_kernel(EsmcLnArgs p) {
   const float* x = p.x + (size_t)row * D;
   float* xo = p.x_out + (size_t)row * D;
   const half_t* y = p.y ? p.y + (size_t)row * D : nullptr;
+  const float* yp = p.yp ? p.yp + (size_t)row * D : nullptr;
+  const size_t plane = (size_t)p.M * D;
   half_t* h = p.h ? p.h + (size_t)row * D : nullptr;
   float* h32 = p.h32 ? p.h32 + (size_t)row * D : nullptr;
   constexpr int MAXV = 8;  // D <= 8 * 4 * 256
@@ -65,8 +68,15 @@ __global__ __launch_bounds__(NTR) void esmc_ln_kernel(EsmcLnArgs p) {
     const int i = 4 * (threadIdx.x + NTR * j);
     if (i < D) {
       f32x4 t = *reinterpret_cast<const f32x4*>(x + i);
-      if (y) {
-        const half4 yy = *reinterpret_cast<const half4*>(y + i);
+      if (y || yp) {
+        half4 yy;
+        if (yp) {  // the linear's split partials, summed in split order and rounded once (as q8_reduce_kernel)
+          f32x4 a = *reinterpret_cast<const f32x4*>(yp + i);
+          for (int sp = 1; sp < p.splits; sp++) a += *reinterpret_cast<const f32x4*>(yp + sp * plane + i);
+          yy = half4{(half_t)a[0], (half_t)a[1], (half_t)a[2], (half_t)a[3]};
+        } else {
+          yy = *reinterpret_cast<const half4*>(y + i);
+        }
 #pragma unroll
         for (int e = 0; e < 4; e++) t[e] += p.alpha * (float)yy[e];
         *reinterpret_cast<f32x4*>(xo + i) = t;

@@ -58,8 +58,8 @@ struct Q8Args {
   half_t* y;            // [M, N]
   int M, K, N;
   int mtiles, ntiles;   // tiles of kQ8TileM x kQ8TileN outputs
-  int splits;           // K ranges per tile (1: no workspace)
-  float* part;          // [splits, M, N] fp32 partials (splits > 1)
+  int splits;           // K ranges per tile
+  float* part;          // [splits, M, N] fp32 partials, or nullptr: y written directly (splits 1)
   const uint32_t* sb;   // packed scales [ntiles, K/64, kQ8TileN] (b << 16 | s), or nullptr
 };
 
@@ -84,6 +84,8 @@ struct TransitionArgs {
 struct EsmcLnArgs {
   const float* x;       // [M, D] fp32 residual
   const half_t* y;      // [M, D] or nullptr: x_out = x + alpha * y
+  const float* yp;      // [splits, M, D] fp32 split-K partials of y, or nullptr: y = fp16(sum in split order)
+  int splits;
   float alpha;
   float* x_out;         // [M, D] (may be x; unused without y)
   const float* w;       // [D]

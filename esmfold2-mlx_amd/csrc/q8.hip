@@ -24,7 +24,9 @@
 // (small grids: M x N too small to fill the GPU), each writes an fp32 partial to the
 // caller's workspace and a second kernel sums the partials in split order (the kernel
 // boundary orders the writes before the reads; no fences or counters): the result does
-// not depend on the order the workgroups ran in.
+// not depend on the order the workgroups ran in. That second kernel is either the
+// reduction here or, for a linear whose output feeds a residual + LayerNorm, the
+// LayerNorm itself (esmc_ln_kernel sums the same partials in the same order).
 #include "common.h"
 #include "kernels.h"
 
@@ -249,7 +251,7 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     for (int w = 1; w < NWQ; w++) v += red[w][blk][r4][lane];
     return v;
   };
-  if (p.splits == 1) {
+  if (p.part == nullptr) {  // one K range per tile: fp16 y directly
     for (int blk = wave; blk < NBLK; blk += NWQ) {
       const int mb = blk / NBQ, nb = blk - mb * NBQ;
       const int m = m0 + 32 * mb + r;
@@ -264,7 +266,8 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     return;
   }
 
-  // Split K: this workgroup's fp32 partial; q8_reduce_kernel sums the splits.
+  // This workgroup's fp32 partial (split sp of p.splits, possibly the only one); q8_reduce_kernel
+  // or the consumer (esmc_ln_kernel) sums the splits.
   float* part = p.part + (size_t)sp * M * N;
   for (int blk = wave; blk < NBLK; blk += NWQ) {
     const int mb = blk / NBQ, nb = blk - mb * NBQ;
@@ -332,7 +335,7 @@ hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s) {
     hipLaunchKernelGGL(q8_linear_kernel<true>, dim3(grid), dim3(NWQ * 64), 0, s, a);
   else
     hipLaunchKernelGGL(q8_linear_kernel<false>, dim3(grid), dim3(NWQ * 64), 0, s, a);
-  if (a.splits > 1) {
+  if (a.part && a.y) {  // partials and an fp16 output: sum them here (no y: the caller's consumer does)
     const size_t plane = (size_t)a.M * a.N, n4 = plane / 4;
     const size_t blocks = (n4 + 255) / 256;
     hipLaunchKernelGGL(q8_reduce_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, s, a.part, a.y,

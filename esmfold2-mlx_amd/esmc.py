@@ -77,12 +77,14 @@ class EsmcBlock(nn.Module):
         qkv = self.wqkv(h)
         q, k, v = kernels.esmc_qk_rope(qkv.view(B * L, 3 * D), self.q_ln, self.k_ln, EPS, B, L, self.n_heads)
         o = kernels.esmc_attention(q, k, v, sid)
-        y = self.wo(o)
-        kernels.esmc_layer_norm(x, self.ln2_w, self.ln2_b, EPS, y=y, alpha=1.0 / res_scale, x_out=x_mid, out=h2)
+        # wo's split-K partials are summed (and rounded to fp16) by the residual + LayerNorm kernel
+        kernels.esmc_layer_norm(x, self.ln2_w, self.ln2_b, EPS, y_parts=self.wo.partials(o), alpha=1.0 / res_scale,
+                                x_out=x_mid, out=h2)
 
-    def ffn(self, h2: torch.Tensor) -> torch.Tensor:
-        """w2(silu(x1) * x2) with [x1 | x2] = w1(h2), fp16 (before the residual's / res_scale)."""
-        return self.w2(kernels.esmc_swiglu(self.w1(h2)))
+    def ffn(self, h2: torch.Tensor):
+        """w2(silu(x1) * x2) with [x1 | x2] = w1(h2) (before the residual's / res_scale), as w2's
+        split-K partials: (partials, splits) for ``esmc_layer_norm(..., y_parts=...)``."""
+        return self.w2.partials(kernels.esmc_swiglu(self.w1(h2)))
 
     def forward(self, x: torch.Tensor, sequence_id=None, res_scale: float = 1.0) -> torch.Tensor:
         """One block on an fp32 residual [B, L, D] (the reference's block_forward, mlx_esmc.py:84-102)."""
@@ -92,7 +94,7 @@ class EsmcBlock(nn.Module):
         self.attention(x, h, _chain_ids(sequence_id, x.device), res_scale, x_mid, h2)
         out = torch.empty_like(x)
         # out = x_mid + y2 / res_scale (the LN output of this call is not needed)
-        kernels.esmc_layer_norm(x_mid, self.ln1_w, self.ln1_b, EPS, y=self.ffn(h2), alpha=1.0 / res_scale,
+        kernels.esmc_layer_norm(x_mid, self.ln1_w, self.ln1_b, EPS, y_parts=self.ffn(h2), alpha=1.0 / res_scale,
                                 x_out=out, out=torch.empty_like(h))
         return out
 
@@ -170,10 +172,10 @@ class HipEsmc(nn.Module):
             y2 = blk.ffn(h2)
             if i + 1 < n:  # second residual into hidden_states[i+1], fused with the next input LN
                 nxt = self.layers[i + 1]
-                kernels.esmc_layer_norm(x_mid, nxt.ln1_w, nxt.ln1_b, EPS, y=y2, alpha=1.0 / self.res_scale,
+                kernels.esmc_layer_norm(x_mid, nxt.ln1_w, nxt.ln1_b, EPS, y_parts=y2, alpha=1.0 / self.res_scale,
                                         x_out=hs[i + 1], out=h)
             else:  # the last block's output is only seen through the final norm (weights only)
-                kernels.esmc_layer_norm(x_mid, self.norm_w, None, EPS, y=y2, alpha=1.0 / self.res_scale,
+                kernels.esmc_layer_norm(x_mid, self.norm_w, None, EPS, y_parts=y2, alpha=1.0 / self.res_scale,
                                         x_out=x_last, out=hs[n], fp32_out=True)
         return hs
 

@@ -7,6 +7,8 @@ torch, passes raw pointers plus the current HIP stream, and raises
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import capi
@@ -110,21 +112,34 @@ def transition(z, ln_w, ln_b, eps, w1, w3, w2=None, out=None):
     return out
 
 
-def esmc_layer_norm(x, w, b, eps, y=None, alpha: float = 1.0, x_out=None, out=None, fp32_out: bool = False):
+def esmc_layer_norm(x, w, b, eps, y=None, alpha: float = 1.0, x_out=None, out=None, fp32_out: bool = False,
+                    y_parts=None):
     """LN over the last axis of the fp32 residual x [M, D] (after x_out = x + alpha*y when y
-    is given) -> fp16 (or fp32) ``out``. Returns out."""
+    is given) -> fp16 (or fp32) ``out``. Returns out. ``y_parts`` = (partials [splits, M, D]
+    fp32, splits) from ``q8_linear_partials`` stands for y = fp16(sum of the partials)."""
     lib = capi.lib()
     _dev(x, "x", torch.float32)
     M, D = x.shape[0] if x.dim() == 2 else x.numel() // x.shape[-1], x.shape[-1]
+    if y is not None and y_parts is not None:
+        raise capi.EsmError(-2, "esmc_layer_norm: y and y_parts are exclusive")
     if y is not None:
         _dev(y, "y", F16)
+    if y_parts is not None:
+        _dev(y_parts[0], "y_parts", torch.float32)
+        if y_parts[0].numel() < int(y_parts[1]) * M * D:
+            raise capi.EsmError(-2, "esmc_layer_norm: y_parts smaller than splits x M x D")
+    if y is not None or y_parts is not None:
         x_out = x if x_out is None else _dev(x_out, "x_out", torch.float32)
     dt = torch.float32 if fp32_out else F16
     out = torch.empty(x.shape, dtype=dt, device=x.device) if out is None else _dev(out, "out", dt)
-    capi.check(lib.esmc_layer_norm(x.data_ptr(), _ptr(y), float(alpha), _ptr(x_out), _dev(w, "w", torch.float32).data_ptr(),
-                                   None if b is None else _dev(b, "b", torch.float32).data_ptr(), float(eps),
-                                   None if fp32_out else out.data_ptr(), out.data_ptr() if fp32_out else None, M, D,
-                                   capi.stream_ptr()))
+    wp, bp = _dev(w, "w", torch.float32).data_ptr(), None if b is None else _dev(b, "b", torch.float32).data_ptr()
+    hp, h32 = (None, out.data_ptr()) if fp32_out else (out.data_ptr(), None)
+    if y_parts is not None:
+        capi.check(lib.esmc_layer_norm_parts(x.data_ptr(), y_parts[0].data_ptr(), int(y_parts[1]), float(alpha),
+                                             _ptr(x_out), wp, bp, float(eps), hp, h32, M, D, capi.stream_ptr()))
+    else:
+        capi.check(lib.esmc_layer_norm(x.data_ptr(), _ptr(y), float(alpha), _ptr(x_out), wp, bp, float(eps), hp, h32,
+                                       M, D, capi.stream_ptr()))
     return out
 
 
@@ -216,6 +231,46 @@ def q8_workspace(M: int, K: int, N: int, device=None):
     if n == 0:
         return None
     return torch.empty(n + 256, dtype=torch.uint8, device=device if device is not None else "cuda")
+
+
+def q8_partials_bytes(M: int, K: int, N: int) -> int:
+    """Bytes of the fp32 partials ``q8_linear_partials`` writes at this shape."""
+    return int(capi.lib().q8_linear_partials_bytes(M, K, N))
+
+
+def q8_partials_buffer(M: int, K: int, N: int, device=None):
+    """A buffer for ``q8_linear_partials`` at this shape (fp32 partials of every split)."""
+    return torch.empty(q8_partials_bytes(M, K, N) + 256, dtype=torch.uint8,
+                       device=device if device is not None else "cuda")
+
+
+def q8_linear_partials(x, q, s, b, parts, group: int = 64, packed=None):
+    """Kernel (d) without its split reduction: returns (partials [splits, M, N] fp32, splits), a view
+    of ``parts`` (a uint8 buffer of at least q8_linear_partials_bytes + 256 bytes, e.g. from
+    ``q8_partials_buffer`` or ``q8_workspace``). fp16(sum over splits in order) is q8_linear's y."""
+    lib = capi.lib()
+    _dev(x, "x", F16)
+    _dev(q, "q", torch.uint8)
+    _dev(s, "s", F16)
+    _dev(b, "b", F16)
+    _dev(parts, "parts", torch.uint8)
+    M, K = x.shape
+    N = q.shape[0]
+    if q.shape[1] != K or s.shape != (N, K // group) or b.shape != s.shape:
+        raise capi.EsmError(-2, f"q8_linear_partials: shapes x{tuple(x.shape)} q{tuple(q.shape)} s{tuple(s.shape)}")
+    off = (-parts.data_ptr()) % 256
+    sbp = None
+    if packed is not None:
+        _dev(packed, "packed", torch.int32)
+        if packed.numel() * 4 < lib.q8_packed_scales_bytes(N, K):
+            raise capi.EsmError(-2, "q8_linear_partials: packed scales too small for this shape")
+        sbp = packed.data_ptr()
+    splits = ctypes.c_int(0)
+    capi.check(lib.q8_linear_partials(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), sbp,
+                                      parts.data_ptr() + off, parts.numel() - off, ctypes.byref(splits), M, K, N,
+                                      group, capi.stream_ptr()))
+    n = splits.value
+    return parts[off:off + 4 * n * M * N].view(torch.float32).view(n, M, N), n
 
 
 def q8_pack_scales(s, b, group: int = 64):

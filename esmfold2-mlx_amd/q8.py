@@ -56,3 +56,16 @@ class Q8Linear(nn.Module):
         y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP, workspace=self._ws[M], packed=self.packed)
         y = y.reshape(*lead, self.out_features)
         return y if x.dtype == torch.float16 else y.to(x.dtype)
+
+    def partials(self, x: torch.Tensor):
+        """(partials [splits, M, N] fp32, splits) of x . W^T for a consumer that sums them in split
+        order (``kernels.esmc_layer_norm(..., y_parts=...)``): rounded to fp16, the sum is
+        ``forward(x)`` bit for bit. The view lives in this layer's per-M buffer (the split-K
+        workspace when the shape splits), valid until the layer's next call."""
+        x2 = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
+        M = x2.shape[0]
+        need = kernels.q8_partials_bytes(M, self.in_features, self.out_features) + 256
+        buf = self._ws.get(M)
+        if buf is None or buf.numel() < need:
+            buf = self._ws[M] = torch.empty(need, dtype=torch.uint8, device=x2.device)
+        return kernels.q8_linear_partials(x2, self.q, self.scales, self.biases, buf, GROUP, packed=self.packed)

@@ -198,6 +198,22 @@ int q8_linear_ws(const esm_half* x, const uint8_t* q, const esm_half* s, const e
 size_t q8_linear_workspace_bytes(int M, int K, int N);
 
 /*
+ * The GEMM of q8_linear_ws without its last step: the fp32 partial sums of y go to
+ * parts [*splits, M, N] (split s covers a contiguous range of K's groups; *splits is the
+ * split count this device's plan uses, 1 when the tiles already fill the GPU) and are
+ * not summed. esmc_layer_norm_parts consumes them, summing in split order and rounding
+ * once to fp16, which gives the bits q8_linear_ws writes to y. Together the two replace,
+ * in the reference, a block's `wo(o)` / `w2(...)` (mx.quantized_matmul, mlx_esmc.py:78-81)
+ * followed by its residual add and LayerNorm (:97-98, :102 and the next block's :91),
+ * without the separate reduction kernel and the fp16 y in between.
+ * parts: q8_linear_partials_bytes(M, K, N) bytes, 256-byte aligned, no initialisation
+ * needed; sb as in q8_linear_ws (NULL allowed).
+ */
+size_t q8_linear_partials_bytes(int M, int K, int N);
+int q8_linear_partials(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, const uint32_t* sb,
+                       float* parts, size_t parts_bytes, int* splits, int M, int K, int N, int group, void* stream);
+
+/*
  * Packs s and b [N, K/group] fp16 into sb [ceil(N/160), K/group, 160] uint32 words
  * (b << 16 | s; rows past N are 0), the layout q8_linear_ws reads a step of in one
  * coalesced load. A layout cache of the reference's fp16 scales/biases
@@ -230,6 +246,14 @@ int q8_pack_scales(const esm_half* s, const esm_half* b, uint32_t* sb, int N, in
  */
 int esmc_layer_norm(const float* x, const esm_half* y, float alpha, float* x_out, const float* w, const float* b,
                     float eps, esm_half* h, float* h_fp32, int M, int D, void* stream);
+/*
+ * esmc_layer_norm with y given as q8_linear_partials' output: y = fp16(sum over s of
+ * y_parts[s]) in split order, then x_out = x + alpha * y and h = LN(x_out) exactly as
+ * above (the same bits as q8_linear_ws followed by esmc_layer_norm). y_parts
+ * [splits, M, D] fp32, 16-byte aligned; splits >= 1; x_out required.
+ */
+int esmc_layer_norm_parts(const float* x, const float* y_parts, int splits, float alpha, float* x_out, const float* w,
+                          const float* b, float eps, esm_half* h, float* h_fp32, int M, int D, void* stream);
 int esmc_qk_rope(const esm_half* qkv, const float* q_ln, const float* k_ln, float eps, esm_half* q, esm_half* k,
                  esm_half* v, int B, int L, int n_heads, int head_dim, float rope_base, void* stream);
 int esmc_attention(const esm_half* q, const esm_half* k, const esm_half* v, const int* sequence_id, esm_half* o, int B,

@@ -72,6 +72,17 @@ def test_rejects_null_and_bad_shapes(lib):
     assert lib.pair_transition(None, None, None, None, 1e-5, None, ctypes.c_void_p(4096), None, 1, 8, 128, 512,
                                None) == -4  # SwiGLU at H=512
     assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 0, 8, 128, 512, None) == 0
+    # the partials entry points: a NULL split count, a short buffer, a bad split count
+    assert lib.q8_linear_partials(None, None, None, None, None, None, 0, None, 4, 128, 64, 64, None) == -1
+    splits = ctypes.c_int(7)
+    assert lib.q8_linear_partials(fake16 := ctypes.c_void_p(4096), fake16, fake16, fake16, None,
+                                  ctypes.c_void_p(1 << 20), 16, ctypes.byref(splits), 5, 1024, 64, 64, None) == -2
+    assert splits.value == 0 and "partials" in _err(lib)
+    assert lib.q8_linear_partials_bytes(5, 1024, 64) >= 5 * 64 * 4 and lib.q8_linear_partials_bytes(5, 100, 64) == 0
+    assert lib.esmc_layer_norm_parts(fake16, fake16, 0, 1.0, fake16, fake16, None, 1e-5, fake16, None, 4, 64,
+                                     None) == -2
+    assert lib.esmc_layer_norm_parts(fake16, None, 2, 1.0, fake16, fake16, None, 1e-5, fake16, None, 4, 64,
+                                     None) == -1
     # a negative or NaN eps is refused by every LayerNorm entry point, before any pointer is used
     for eps in (-1e-5, float("nan")):
         assert lib.pair_transition(None, None, None, None, eps, None, None, None, 1, 8, 128, 512, None) == -2

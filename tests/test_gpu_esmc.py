@@ -85,6 +85,36 @@ def test_swiglu(gpu_lib, pkg):
     assert float((y - ref).abs().max()) <= 2 ** -10 * float(ref.abs().max())
 
 
+@pytest.mark.parametrize("M,K,N", [(238, 2560, 2560), (238, 5120, 2560), (238, 2560, 10240), (37, 256, 256),
+                                   (5, 1024, 64)])
+def test_q8_partials_then_layer_norm_equal_unfused(gpu_lib, pkg, M, K, N):
+    """q8_linear_partials + esmc_layer_norm_parts give the same bits as q8_linear (with its split-K
+    workspace) + esmc_layer_norm: the partials summed in split order and rounded once, then the same
+    residual add and LayerNorm. Covers split (M=238, N=2560) and unsplit (N=10240) plans."""
+    g = _gen(M + K + N)
+    p = oe.quantize(torch.randn(N, K, generator=g) * K ** -0.5)
+    lin = pkg.q8.Q8Linear(torch.from_numpy(p.q), torch.from_numpy(p.s), torch.from_numpy(p.b))
+    x = torch.randn(M, K, generator=g).half().to(DEV)
+    y = lin(x)
+    parts, splits = lin.partials(x)
+    assert parts.shape == (splits, M, N) and splits >= 1
+    acc = parts[0].clone()
+    for s_ in range(1, splits):
+        acc += parts[s_]
+    assert torch.equal(acc.half(), y)
+    if N > 8192:  # wider than the LayerNorm supports: the partials alone are the case
+        return
+    r = (3 * torch.randn(M, N, generator=g) + 1).to(DEV)
+    w, b = (1 + 0.1 * torch.randn(N, generator=g)).to(DEV), (0.1 * torch.randn(N, generator=g)).to(DEV)
+    for fp32_out in (False, True):
+        xo1, xo2 = torch.empty_like(r), torch.empty_like(r)
+        h1 = pkg.kernels.esmc_layer_norm(r, w, b, 1e-5, y=y, alpha=0.37, x_out=xo1, fp32_out=fp32_out)
+        h2 = pkg.kernels.esmc_layer_norm(r, w, b, 1e-5, y_parts=(parts, splits), alpha=0.37, x_out=xo2,
+                                         fp32_out=fp32_out)
+        torch.cuda.synchronize()
+        assert torch.equal(xo1, xo2) and torch.equal(h1, h2)
+
+
 def _weights(D, F_, seed):
     g = _gen(seed)
     r = lambda *s: torch.randn(*s, generator=g)  # noqa: E731
