@@ -26,9 +26,9 @@ Also reported on the same JSON line:
                 launches, beside it;
   cpu_baseline  the CPU oracle (torch fp32 restatement of the reference's
                 _trimul_forward) on the host cores, a bounded sample of the same
-                workload (rank 0, N=1 only). This leg is also the checker: the
-                benchmarked pair output and sampled q8 rows are compared with the
-                oracle's (the GPU leg itself imports nothing from oracle/).
+                workload (rank 0, N=1 only). This leg also verifies the GPU leg:
+                the benchmarked pair output and sampled q8 rows are compared with
+                the oracle's (the GPU leg itself imports nothing from oracle/).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--graph]
 """
@@ -109,7 +109,7 @@ def copy_probe(dev, reps: int = 10, nbytes: int = 64 << 20):
 
 def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=None):
     """The CPU oracle in fp32 on the host cores: 1 warm-up, median of 3 TMU pairs at L=238.
-    Also the checker of the GPU leg: the benchmarked pair output against the oracle's
+    It also verifies the GPU leg: the benchmarked pair output against the oracle's
     (max|err| / RMS(update), bar 1e-2) and the sampled q8 rows (normwise, bar 1e-3)."""
     import numpy as np
     import torch
@@ -175,7 +175,7 @@ def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=Non
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        print(json.dumps({"error": "the TMU path is measured on one GPU (its sharding is not built); --gpus must be 1"}))
         sys.exit(2)
     import torch
     from __graft_entry__ import load_package

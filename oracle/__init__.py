@@ -1,7 +1,7 @@
 """CPU oracle for the triangle multiplicative update, the pair trunk and the 8-bit ESMC linear.
 
 THIS PACKAGE IS TEST INFRASTRUCTURE. It is a CPU restatement of the reference's
-arithmetic, used only as the checker: by ``tests/``, by
+arithmetic, used only to verify results: by ``tests/``, by
 ``__graft_entry__.smoke()`` and by ``bench.py``'s ``cpu_baseline`` leg. The
 product path (the HIP kernels behind the C ABI in ``esmfold2-mlx_amd/``) never
 imports, calls or falls back to anything here.

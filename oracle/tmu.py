@@ -1,7 +1,7 @@
 """Oracle: the triangle multiplicative update (TMU), restated on the CPU in torch.
 
-TEST INFRASTRUCTURE ONLY (see oracle/__init__.py): the checker for the HIP path
-and the timed CPU baseline, never part of the product.
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py): the reference the HIP path is
+verified against and the timed CPU baseline, never part of the product.
 
 Reference arithmetic restated here (paths relative to the reference repo):
   fast_trunk.py:19-32      _trimul_forward: LN_in -> split-weight projections ->
