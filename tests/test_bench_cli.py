@@ -1,0 +1,27 @@
+"""bench.py's contract pieces that need no GPU: the one-GPU guard and the committed counter
+summary it reads for ``roofline.traffic``."""
+
+import json
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120, cwd=ROOT)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]
+
+
+def test_counter_summary_has_every_tmu_kernel():
+    import bench
+
+    t = bench.measured_traffic()
+    for k in ("tmu_project_kernel", "tmu_contract_kernel", "tmu_epilogue_kernel"):
+        # one TMU launch moves 43.5 MB algorithmically; the measured traffic stays within 15% of it
+        assert 0.95 * 43.5e6 < t[k] < 1.15 * 43.5e6, (k, t.get(k))
