@@ -107,6 +107,28 @@ def copy_probe(dev, reps: int = 10, nbytes: int = 64 << 20):
     torch.cuda.synchronize()
 
 
+def host_threads() -> int:
+    """The host cores this process may use: its CPU affinity, capped by OMP_NUM_THREADS when set
+    (the share of a shared host the job is given)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        cap = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        cap = 0
+    return max(1, min(n, cap) if cap > 0 else n)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=None):
     """The CPU oracle in fp32 on the host cores: 1 warm-up, median of 3 TMU pairs at L=238.
     It also verifies the GPU leg: the benchmarked pair output against the oracle's
@@ -114,6 +136,8 @@ def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=Non
     import numpy as np
     import torch
     from oracle import q8 as oq8, tmu
+    threads = host_threads()
+    torch.set_num_threads(threads)
     threads = torch.get_num_threads()
     zf = z.float()
     fields = ("w_bundle", "w_emit", "w_gate", "ln_in_w", "ln_in_b", "ln_mix_w", "ln_mix_b", "ln_in_eps", "ln_mix_eps",
@@ -137,19 +161,23 @@ def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=Non
     ok = pair_err <= 1e-2 and all(e <= 1e-3 for e in q8_err.values())
     stack_err = None
     if stack_case is not None:
-        # the block stack against the oracle with an fp16 residual stream (fp32, CPU)
+        # the block stack against the oracle in fp64 (exact arithmetic, fp64 stream). The bar is
+        # max 3e-2 and RMS 1e-2 of RMS(update): at this depth the reference's own fp16 scheme sits
+        # at max 1.75e-2 from fp64 (oracle.transition.stack_forward_fp16ref), above 1e-2
         from oracle import transition as otr
         zs, blocks, got = stack_case
-        ob = [otr.BlockWeights(tmu.TriMulWeights(**{f: getattr(a, f) for f in fields}),
-                               tmu.TriMulWeights(**{f: getattr(b, f) for f in fields}),
-                               otr.TransitionWeights(t.ln_w, t.ln_b, t.w1, t.w3, t.w2, eps=t.eps))
+        ob = [otr.BlockWeights(tmu.TriMulWeights(**{f: getattr(a, f) for f in fields}).to(torch.float64),
+                               tmu.TriMulWeights(**{f: getattr(b, f) for f in fields}).to(torch.float64),
+                               otr.TransitionWeights(t.ln_w.double(), t.ln_b.double(), t.w1.double(), t.w3.double(),
+                                                     None if t.w2 is None else t.w2.double(), eps=t.eps))
               for a, b, t in blocks]
         with torch.no_grad():
-            ref = otr.stack_forward(zs.float(), None, ob, 3, store=torch.float16).double()
+            ref = otr.stack_forward(zs.double(), None, ob, 3)
         u = ref - zs.double()
         d = got.double() - ref
         rms = float(u.pow(2).mean().sqrt())
-        stack_err = {"max_err_over_rms": float(d.abs().max()) / rms, "rms_err_over_rms": float(d.pow(2).mean().sqrt()) / rms}
+        stack_err = {"max_err_over_rms": float(d.abs().max()) / rms, "rms_err_over_rms": float(d.pow(2).mean().sqrt()) / rms,
+                     "reference": "fp64 oracle", "bar": {"max": 3e-2, "rms": 1e-2}}
         ok = ok and stack_err["max_err_over_rms"] <= 3e-2 and stack_err["rms_err_over_rms"] <= 1e-2
     esmc_err = None
     if esmc_case is not None:
@@ -165,10 +193,11 @@ def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=Non
         esmc_err = float((got.double() - ref).abs().max()) / float(u.pow(2).mean().sqrt())
         ok = ok and esmc_err <= 1e-2
     return {"value": L * L / t, "unit": "cells/s", "cores": threads, "kind": "port",
+            "cpu": cpu_model(), "host_cpus": os.cpu_count(), "torch_threads": threads,
             "sample": f"TMU pair (out+in, residuals) at L={L}, C=c={C}, fp32 torch on CPU, median of 3 after 1 "
                       f"warm-up, {t * 1e3:.1f} ms per pair",
             "check": {"pair_max_err_over_rms": pair_err, "q8_rel_err_sample_rows": q8_err,
-                      "block_stack_vs_oracle_fp16_stream": stack_err, "esmc_block_max_err_over_rms": esmc_err,
+                      "block_stack_vs_oracle_fp64": stack_err, "esmc_block_max_err_over_rms": esmc_err,
                       "ok": ok}}
 
 
@@ -442,6 +471,7 @@ def main():
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             yg = blk(xed, None, res_scale=rs)
+        held = pkg.scratch.current(dev)  # the shared scratch the captured launches use stays alive
         replays_equal = True
         ts = []
         for _ in range(5):

@@ -13,19 +13,23 @@ Modules:
   var_hip_trimul   -- the reference-style variant plugin for the TMUs: apply(model)
   var_hip_trunk    -- the variant plugin replacing the whole folding trunk: apply(model)
   var_6b_hip_trunks -- the variant plugin replacing all four trunk stacks of the 6B model
+  var_6b_hip_loop  -- the variant plugin installing the 6B parcae recycling loop (optional early exit)
+  var_6b_hip_adaptive -- that loop with the reference's early-exit policy
+  var_hip_adaptive_loops -- adaptive recycling of the folding trunk (AdaptiveTrunk)
+  scratch          -- the device scratch buffer every module shares
   variants         -- apply_variants(model, names): the plugins by name, in order
   workloads        -- seeded synthetic inputs of the benchmark configurations
 """
 
 from . import build, capi  # noqa: F401
 
-__all__ = ["build", "capi", "kernels", "trimul", "q8", "esmc", "trunk", "recycle", "var_hip_trimul", "var_hip_trunk",
-           "var_6b_hip_trunks", "variants", "workloads"]
+__all__ = ["build", "capi", "kernels", "trimul", "q8", "esmc", "trunk", "recycle", "scratch", "var_hip_trimul",
+           "var_hip_trunk", "var_6b_hip_trunks", "var_6b_hip_loop", "var_6b_hip_adaptive", "var_hip_adaptive_loops",
+           "variants", "workloads"]
 
 
 def __getattr__(name):
-    if name in ("kernels", "trimul", "q8", "esmc", "trunk", "recycle", "var_hip_trimul", "var_hip_trunk",
-                "var_6b_hip_trunks", "variants", "workloads"):
+    if name in __all__[2:]:
         import importlib
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)

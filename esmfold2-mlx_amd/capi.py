@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import sys
 import threading
 
 from . import build as _build
@@ -19,6 +20,7 @@ _vp, _int, _f32, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_s
 SIGNATURES = {
     "esm_last_error": (ctypes.c_char_p, []),
     "esm_version": (ctypes.c_char_p, []),
+    "esm_source_hash": (ctypes.c_char_p, []),
     "tmu_workspace_bytes": (_sz, [_int, _int, _int]),
     "tmu_leading_dim": (_int, [_int]),
     "tmu_project": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp]),
@@ -44,6 +46,7 @@ SIGNATURES = {
     "q8_packed_scales_bytes": (_sz, [_int, _int]),
     "q8_pack_scales": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp]),
     "q8_dequant": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
+    "q8_quantize": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
 }
 
 ERRORS = {-1: "ESM_ERR_NULL", -2: "ESM_ERR_SHAPE", -3: "ESM_ERR_ALIGN", -4: "ESM_ERR_UNSUPPORTED",
@@ -58,28 +61,46 @@ class EsmError(RuntimeError):
 
 _lock = threading.Lock()
 _lib = None
+_gpu_ok = False
 
 
 def lib_path() -> str:
     return _build.LIB_PATH
 
 
+def _load() -> ctypes.CDLL:
+    """Load the in-tree library, building it first when it is missing or was compiled from other
+    sources than the ones beside it (compared by content hash, so copies keep their state)."""
+    if not _build.up_to_date():
+        stale = os.path.exists(_build.LIB_PATH)
+        if stale:
+            print(f"[esmfold2_amd] {_build.LIB_PATH} was built from other sources: rebuilding", file=sys.stderr,
+                  flush=True)
+        _build.build(force=True)
+    handle = ctypes.CDLL(_build.LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)  # AttributeError if a declared symbol is missing
+        fn.restype, fn.argtypes = res, args
+    if handle.esm_source_hash().decode() != _build.source_hash():
+        raise EsmError(-5, f"{_build.LIB_PATH} does not match its sources after the build")
+    return handle
+
+
 def lib(reload: bool = False, require_gpu: bool = True) -> ctypes.CDLL:
-    """The loaded library. Builds it only if no built library exists."""
-    global _lib
+    """The loaded library (built on first use when missing or stale). With ``require_gpu`` the
+    first call checks that a ROCm GPU is visible; later calls return the cached handle."""
+    global _lib, _gpu_ok
+    h = _lib
+    if h is not None and not reload and (_gpu_ok or not require_gpu):
+        return h
     with _lock:
         if _lib is None or reload:
-            if not os.path.exists(_build.LIB_PATH):
-                _build.build(force=True)
-            handle = ctypes.CDLL(_build.LIB_PATH)
-            for name, (res, args) in SIGNATURES.items():
-                fn = getattr(handle, name)  # AttributeError if a declared symbol is missing
-                fn.restype, fn.argtypes = res, args
-            _lib = handle
-    if require_gpu:
-        import torch
-        if not torch.cuda.is_available():
-            raise EsmError(-5, "no ROCm GPU visible: the HIP path has no CPU fallback")
+            _lib = _load()
+        if require_gpu and not _gpu_ok:
+            import torch
+            if not torch.cuda.is_available():
+                raise EsmError(-5, "no ROCm GPU visible: the HIP path has no CPU fallback")
+            _gpu_ok = True
     return _lib
 
 

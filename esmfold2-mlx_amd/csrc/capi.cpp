@@ -79,6 +79,13 @@ Q8Plan q8_plan(int M, int K, int N) {
   return p;
 }
 
+#ifndef ESM_SOURCE_HASH
+#define ESM_SOURCE_HASH "unknown"
+#endif
+// The content hash of the sources this library was built from, also findable as a tagged
+// string in the file itself, so a loader can tell a stale build without loading it.
+__attribute__((used)) const char kSourceTag[] = "ESMSRC:" ESM_SOURCE_HASH;
+
 using esm::half_t;
 inline const half_t* H(const esm_half* p) { return reinterpret_cast<const half_t*>(p); }
 inline half_t* H(esm_half* p) { return reinterpret_cast<half_t*>(p); }
@@ -91,7 +98,9 @@ extern "C" {
 
 const char* esm_last_error(void) { return g_err.c_str(); }
 
-const char* esm_version(void) { return "esmfold2_amd 0.1.0 gfx950"; }
+const char* esm_version(void) { return "esmfold2_amd 0.2.0 gfx950"; }
+
+const char* esm_source_hash(void) { return kSourceTag + 7; }
 
 int tmu_leading_dim(int L) { return L <= 0 ? 0 : round_up(L, 8); }
 
@@ -132,8 +141,11 @@ int tmu_contract(const esm_half* a, const esm_half* b, esm_half* x, int batch, i
   if (batch == 0 || L == 0) return ok();
   if (!a || !b || !x) return fail(ESM_ERR_NULL, "tmu_contract: NULL pointer");
   if (L > kMaxL || batch > 65535) return fail(ESM_ERR_SHAPE, "tmu_contract: L=%d batch=%d out of range", L, batch);
-  if (ld % 8 != 0 || ld < L || ldx % 8 != 0 || ldx < L)
-    return fail(ESM_ERR_SHAPE, "tmu_contract: ld=%d ldx=%d must be multiples of 8 and >= L=%d", ld, ldx, L);
+  // x columns [L, ldx) are written with zeros; the output blocks cover every column below
+  // roundup(L, 64), so ldx may not exceed it.
+  if (ld % 8 != 0 || ld < L || ldx % 8 != 0 || ldx < L || ldx > round_up(L, 64))
+    return fail(ESM_ERR_SHAPE, "tmu_contract: ld=%d ldx=%d must be multiples of 8, >= L=%d, ldx <= %d", ld, ldx, L,
+                round_up(L, 64));
   if (!aligned16(a) || !aligned16(b) || !aligned16(x))
     return fail(ESM_ERR_ALIGN, "tmu_contract: a, b, x must be 16-byte aligned");
   esm::ContractArgs args{H(a), H(b), H(x), batch, L, ld, ldx, scale};
@@ -422,6 +434,18 @@ size_t q8_linear_workspace_bytes(int M, int K, int N) {
   if (M <= 0 || K <= 0 || N <= 0 || K % 64 != 0 || N % 64 != 0 || K > kQ8MaxK) return 0;
   const Q8Plan pl = q8_plan(M, K, N);
   return pl.splits > 1 ? pl.bytes : 0;
+}
+
+int q8_quantize(const float* w, uint8_t* q, esm_half* s, esm_half* b, int N, int K, int group, void* stream) {
+  if (N < 0 || K < 0) return fail(ESM_ERR_SHAPE, "q8_quantize: N=%d K=%d must be >= 0", N, K);
+  if (group != 64) return fail(ESM_ERR_UNSUPPORTED, "q8_quantize: group=%d (supported: 64)", group);
+  if (N == 0 || K == 0) return ok();
+  if (K % 64 != 0) return fail(ESM_ERR_SHAPE, "q8_quantize: K=%d must be a multiple of 64", K);
+  if (!w || !q || !s || !b) return fail(ESM_ERR_NULL, "q8_quantize: NULL pointer");
+  if (!aligned16(w) || (reinterpret_cast<uintptr_t>(q) & 3u) || (reinterpret_cast<uintptr_t>(s) & 1u) ||
+      (reinterpret_cast<uintptr_t>(b) & 1u))
+    return fail(ESM_ERR_ALIGN, "q8_quantize: w must be 16-byte, q 4-byte, s and b 2-byte aligned");
+  return hip_status(esm::launch_q8_quantize(w, q, H(s), H(b), N, K, (hipStream_t)stream), "q8_quantize launch");
 }
 
 int q8_dequant(const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* w, int N, int K, int group,

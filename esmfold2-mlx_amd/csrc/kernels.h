@@ -162,6 +162,7 @@ hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s);
 hipError_t launch_esmc_attention(const EsmcAttnArgs& a, hipStream_t s);
 hipError_t launch_esmc_swiglu(const half_t* x12, half_t* y, size_t M, int F, hipStream_t s);
 hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st);
+hipError_t launch_q8_quantize(const float* w, uint8_t* q, half_t* s, half_t* b, int N, int K, hipStream_t st);
 hipError_t launch_q8_dequant(const uint8_t* q, const half_t* s, const half_t* b, half_t* w, int N, int K,
                              hipStream_t st);
 

@@ -344,6 +344,58 @@ hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// MLX's affine 8-bit quantisation of fp32 weights W [N, K] along K, groups of 64 (the
+// quantiser of layer_params, mlx_esmc.py:70-74): per group, scale = max((max - min) / 255,
+// 1e-7) signed towards the larger-magnitude extreme (the edge), q0 = rint(edge / scale);
+// unless q0 = 0 the scale becomes edge / q0 and the bias the edge (0 lands on the grid),
+// else the bias is 0; codes clamp(rint((w - bias) / scale), 0, 255). fp32 arithmetic with
+// IEEE division, rint = round half to even; scales and biases leave rounded to fp16.
+// Sixteen lanes own one group (4 values each, one 16-byte load): min / max over the 16
+// lanes, then 4 codes packed into one 4-byte store per lane.
+__global__ __launch_bounds__(256) void q8_quantize_kernel(const float* __restrict__ w, uint8_t* __restrict__ q,
+                                                          half_t* __restrict__ s, half_t* __restrict__ b,
+                                                          size_t ngroups) {
+  const int sub = threadIdx.x & 15;
+  const size_t step = ((size_t)gridDim.x * blockDim.x) >> 4;
+  for (size_t gi = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; gi < ngroups; gi += step) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(w + gi * QG + 4 * sub);
+    float lo = fminf(fminf(v[0], v[1]), fminf(v[2], v[3]));
+    float hi = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) {  // the 16 lanes of this group only
+      lo = fminf(lo, __shfl_xor(lo, m, 16));
+      hi = fmaxf(hi, __shfl_xor(hi, m, 16));
+    }
+    const bool lo_edge = fabsf(lo) > fabsf(hi);
+    float scale = fmaxf((hi - lo) / 255.0f, 1e-7f);
+    scale = lo_edge ? scale : -scale;
+    const float edge = lo_edge ? lo : hi;
+    const float q0 = __builtin_rintf(edge / scale);
+    const bool at_zero = q0 == 0.0f;
+    scale = at_zero ? scale : edge / q0;
+    const float bias = at_zero ? 0.0f : edge;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float c = fminf(fmaxf(__builtin_rintf((v[e] - bias) / scale), 0.0f), 255.0f);
+      packed |= (uint32_t)c << (8 * e);
+    }
+    *reinterpret_cast<uint32_t*>(q + gi * QG + 4 * sub) = packed;
+    if (sub == 0) {
+      s[gi] = (half_t)scale;
+      b[gi] = (half_t)bias;
+    }
+  }
+}
+
+hipError_t launch_q8_quantize(const float* w, uint8_t* q, half_t* s, half_t* b, int N, int K, hipStream_t st) {
+  const size_t ngroups = (size_t)N * (K / QG);
+  const size_t blocks = (ngroups * 16 + 255) / 256;
+  const int grid = (int)(blocks < 8192 ? blocks : 8192);
+  hipLaunchKernelGGL(q8_quantize_kernel, dim3(grid), dim3(256), 0, st, w, q, s, b, ngroups);
+  return hipGetLastError();
+}
+
 hipError_t launch_q8_dequant(const uint8_t* q, const half_t* s, const half_t* b, half_t* w, int N, int K,
                              hipStream_t st) {
   const size_t nchunks = (size_t)N * K / 16;

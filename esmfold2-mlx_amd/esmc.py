@@ -14,6 +14,8 @@ hidden_states[i + 1], fused with the next block's input LayerNorm (or the final 
 from __future__ import annotations
 
 import math
+import os
+import re
 from types import SimpleNamespace
 
 import torch
@@ -24,6 +26,35 @@ from .q8 import Q8Linear
 
 EPS = 1e-5
 LINEARS = ("wqkv", "wo", "w1", "w2")
+NORMS = ("ln1_w", "ln1_b", "q_ln", "k_ln", "ln2_w", "ln2_b")
+# every array of one layer in the converted-weight cache: the norms, then per linear the
+# packed codes and their fp16 scales and biases (mlx_esmc.py:53-75)
+CACHE_NAMES = NORMS + tuple(f"{n}{t}" for n in LINEARS for t in ("", "_s", "_b"))
+# HF names of the published fp32 checkpoint, per layer (mlx_esmc.py:56-67): each cache
+# linear is the row-wise concatenation of these (q, k, v for wqkv; gate then up for w1)
+HF_LINEARS = {
+    "wqkv": ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight"),
+    "wo": ("self_attn.o_proj.weight",),
+    "w1": ("mlp.gate_proj.weight", "mlp.up_proj.weight"),
+    "w2": ("mlp.down_proj.weight",),
+}
+HF_NORMS = {"ln1_w": "input_layernorm.weight", "ln1_b": "input_layernorm.bias", "q_ln": "self_attn.q_norm.weight",
+            "k_ln": "self_attn.k_norm.weight", "ln2_w": "post_attention_layernorm.weight",
+            "ln2_b": "post_attention_layernorm.bias"}
+_LAYER_KEY = re.compile(r"layers\.(\d+)\.([A-Za-z0-9_]+)")
+
+
+def hf_layer(tensors, i: int, device=None) -> tuple[dict, dict]:
+    """One block from the published HF-named fp32 tensors (``tensors[f"esmc.layers.{i}.{name}"]``):
+    (LayerNorm parameters by cache name, {linear: Q8Linear}), each linear quantised on the GPU
+    from fp32 with MLX's affine 8-bit scheme (layer_params, mlx_esmc.py:53-75)."""
+    get = lambda name: tensors[f"esmc.layers.{i}.{name}"]  # noqa: E731
+    ln = {n: get(h).detach().float() for n, h in HF_NORMS.items()}
+    lin = {}
+    for n, parts in HF_LINEARS.items():
+        w = torch.cat([get(h).detach().float() for h in parts]) if len(parts) > 1 else get(parts[0]).detach().float()
+        lin[n] = Q8Linear.from_float(w, device=device)
+    return ln, lin
 
 
 class EsmcBlock(nn.Module):
@@ -62,7 +93,7 @@ class EsmcBlock(nn.Module):
 
     def params(self) -> dict:
         """The layer's arrays under the reference's names (inverse of ``from_params``)."""
-        p = {n: getattr(self, n).detach().cpu() for n in ("ln1_w", "ln1_b", "q_ln", "k_ln", "ln2_w", "ln2_b")}
+        p = {n: getattr(self, n).detach().cpu() for n in NORMS}
         for n in LINEARS:
             lin = getattr(self, n)
             q = lin.q.detach().cpu().contiguous()
@@ -127,18 +158,57 @@ class HipEsmc(nn.Module):
     # ---- construction: the reference's converted-weight cache (mlx_esmc.py:116-148) -------------
     @classmethod
     def from_cache(cls, path, n_heads: int = 40, device=None) -> "HipEsmc":
-        """From a safetensors file with the reference's layout: "embed", "norm_w" and
-        "layers.{i}.{name}" for every name of ``EsmcBlock.from_params`` (8-bit caches)."""
+        """From a safetensors file in the reference's converted-weight layout (mlx_esmc.py:116-148):
+        "embed" [V, D] and "norm_w" [D] fp32, and for layers 0 .. n-1 every name of
+        ``CACHE_NAMES`` under "layers.{i}." (8-bit codes as uint32 words, four per word)."""
         from safetensors.torch import load_file
         flat = load_file(str(path))
-        n = 1 + max(int(k.split(".")[1]) for k in flat if k.startswith("layers."))
-        per = [{} for _ in range(n)]
-        for k, v in flat.items():
-            if k.startswith("layers."):
-                _, i, name = k.split(".", 2)
-                per[int(i)][name] = v
-        layers = [EsmcBlock.from_params(p, n_heads, device=device) for p in per]
+        per_layer: dict[int, dict] = {}
+        for key, t in flat.items():
+            m = _LAYER_KEY.fullmatch(key)
+            if m is not None:
+                per_layer.setdefault(int(m.group(1)), {})[m.group(2)] = t
+            elif key not in ("embed", "norm_w"):
+                raise ValueError(f"{path}: unexpected key {key!r} in an ESMC cache")
+        for key in ("embed", "norm_w"):
+            if key not in flat:
+                raise ValueError(f"{path}: missing {key!r}")
+        n = len(per_layer)
+        if n == 0 or sorted(per_layer) != list(range(n)):
+            raise ValueError(f"{path}: layer indices {sorted(per_layer)[:8]}... are not 0..{n - 1}")
+        for i in range(n):
+            missing = [c for c in CACHE_NAMES if c not in per_layer[i]]
+            extra = [c for c in per_layer[i] if c not in CACHE_NAMES]
+            if missing or extra:
+                raise ValueError(f"{path}: layer {i} missing {missing}, unexpected {extra}")
+        layers = [EsmcBlock.from_params(per_layer[i], n_heads, device=device) for i in range(n)]
         return cls(flat["embed"], layers, flat["norm_w"], n_heads, device=device)
+
+    @classmethod
+    def from_hf(cls, tensors, n_layers: int | None = None, n_heads: int = 40, cache=None,
+                device=None) -> "HipEsmc":
+        """From the published fp32 checkpoint's HF-named tensors (any mapping, e.g. a dict or a
+        lazy shard reader: "esmc.embed_tokens.weight", "esmc.norm.weight",
+        "esmc.layers.{i}.…"), every linear quantised to 8 bits on the GPU (the reference's
+        from_shards, mlx_esmc.py:116-137). With ``cache`` (a path): load it when it exists,
+        otherwise convert and write it there in the layout ``from_cache`` reads."""
+        if cache is not None and os.path.exists(str(cache)):
+            return cls.from_cache(cache, n_heads, device=device)
+        if n_layers is None:
+            idx = {int(m.group(1)) for k in tensors.keys()
+                   if (m := re.match(r"esmc\.layers\.(\d+)\.", k)) is not None}
+            n_layers = len(idx)
+        layers = []
+        for i in range(n_layers):
+            ln, lin = hf_layer(tensors, i, device=device)
+            layers.append(EsmcBlock(ln["ln1_w"], ln["ln1_b"], ln["q_ln"], ln["k_ln"], ln["ln2_w"], ln["ln2_b"],
+                                    lin["wqkv"], lin["wo"], lin["w1"], lin["w2"], n_heads, device=device))
+        esmc = cls(tensors["esmc.embed_tokens.weight"].detach().float(), layers,
+                   tensors["esmc.norm.weight"].detach().float(), n_heads, device=device)
+        if cache is not None:
+            os.makedirs(os.path.dirname(os.path.abspath(str(cache))), exist_ok=True)
+            esmc.save_cache(cache)
+        return esmc
 
     def save_cache(self, path) -> None:
         from safetensors.torch import save_file

@@ -30,6 +30,16 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
+def _out(t: torch.Tensor, name: str, dtype, numel: int) -> torch.Tensor:
+    """A caller-provided output or auxiliary tensor: device, dtype, contiguity, and exactly the
+    number of elements the kernel writes (a raw pointer carries no size, so an undersized
+    tensor would take out-of-bounds device writes)."""
+    _dev(t, name, dtype)
+    if t.numel() != numel:
+        raise capi.EsmError(-2, f"{name} has {t.numel()} elements, the kernel writes {numel}")
+    return t
+
+
 def leading_dim(L: int) -> int:
     return capi.lib().tmu_leading_dim(L)
 
@@ -48,7 +58,7 @@ def project(z, mask, ln_w, ln_b, eps, w, incoming: bool, ld: int | None = None):
     a = torch.empty(B, c, L, ld, dtype=F16, device=z.device)
     b = torch.empty_like(a)
     if mask is not None:
-        _dev(mask, "mask", F16)
+        _out(mask, "mask", F16, B * L * L)
     capi.check(lib.tmu_project(z.data_ptr(), _ptr(mask), _dev(ln_w, "ln_w", torch.float32).data_ptr(),
                                _dev(ln_b, "ln_b", torch.float32).data_ptr(), float(eps), _dev(w, "w", F16).data_ptr(),
                                a.data_ptr(), b.data_ptr(), B, L, C, c, ld, int(incoming), capi.stream_ptr()))
@@ -77,9 +87,9 @@ def epilogue(x, z, mask, ln_in_w, ln_in_b, eps_in, ln_mix_w, ln_mix_b, eps_mix, 
     _dev(z, "z", F16)
     B, L, _, C = z.shape
     c = w_emit.shape[1]
-    out = torch.empty_like(z) if out is None else _dev(out, "out", F16)
+    out = torch.empty_like(z) if out is None else _out(out, "out", F16, z.numel())
     if mask is not None:
-        _dev(mask, "mask", F16)
+        _out(mask, "mask", F16, B * L * L)
     capi.check(lib.tmu_epilogue(x.data_ptr(), x.shape[-1], z.data_ptr(), _ptr(mask),
                                 _dev(ln_in_w, "ln_in_w", torch.float32).data_ptr(),
                                 _dev(ln_in_b, "ln_in_b", torch.float32).data_ptr(), float(eps_in),
@@ -105,7 +115,7 @@ def transition(z, ln_w, ln_b, eps, w1, w3, w2=None, out=None):
         _dev(w2, "w2", F16)
     if tuple(w1.shape) != (H, C) or tuple(w3.shape) != (C, H) or (w2 is not None and tuple(w2.shape) != (H, C)):
         raise capi.EsmError(-2, f"transition: w1 {tuple(w1.shape)}, w3 {tuple(w3.shape)} for C={C}")
-    out = torch.empty_like(z) if out is None else _dev(out, "out", F16)
+    out = torch.empty_like(z) if out is None else _out(out, "out", F16, z.numel())
     capi.check(lib.pair_transition(z.data_ptr(), out.data_ptr(), _dev(ln_w, "ln_w", torch.float32).data_ptr(),
                                    _dev(ln_b, "ln_b", torch.float32).data_ptr(), float(eps), w1.data_ptr(), _ptr(w2),
                                    w3.data_ptr(), B, L, C, H, capi.stream_ptr()))
@@ -123,15 +133,15 @@ def esmc_layer_norm(x, w, b, eps, y=None, alpha: float = 1.0, x_out=None, out=No
     if y is not None and y_parts is not None:
         raise capi.EsmError(-2, "esmc_layer_norm: y and y_parts are exclusive")
     if y is not None:
-        _dev(y, "y", F16)
+        _out(y, "y", F16, M * D)
     if y_parts is not None:
         _dev(y_parts[0], "y_parts", torch.float32)
         if y_parts[0].numel() < int(y_parts[1]) * M * D:
             raise capi.EsmError(-2, "esmc_layer_norm: y_parts smaller than splits x M x D")
     if y is not None or y_parts is not None:
-        x_out = x if x_out is None else _dev(x_out, "x_out", torch.float32)
+        x_out = x if x_out is None else _out(x_out, "x_out", torch.float32, M * D)
     dt = torch.float32 if fp32_out else F16
-    out = torch.empty(x.shape, dtype=dt, device=x.device) if out is None else _dev(out, "out", dt)
+    out = torch.empty(x.shape, dtype=dt, device=x.device) if out is None else _out(out, "out", dt, M * D)
     wp, bp = _dev(w, "w", torch.float32).data_ptr(), None if b is None else _dev(b, "b", torch.float32).data_ptr()
     hp, h32 = (None, out.data_ptr()) if fp32_out else (out.data_ptr(), None)
     if y_parts is not None:
@@ -148,7 +158,12 @@ def esmc_qk_rope(qkv, q_ln, k_ln, eps, B: int, L: int, n_heads: int, base: float
     lib = capi.lib()
     _dev(qkv, "qkv", F16)
     shape = (B, n_heads, L, 64)
-    q, k, v = out if out is not None else tuple(torch.empty(shape, dtype=F16, device=qkv.device) for _ in range(3))
+    if qkv.numel() != B * L * 3 * n_heads * 64:
+        raise capi.EsmError(-2, f"esmc_qk_rope: qkv has {qkv.numel()} elements for B={B} L={L} heads={n_heads}")
+    if out is not None:
+        q, k, v = (_out(t, n, F16, B * n_heads * L * 64) for t, n in zip(out, ("q", "k", "v")))
+    else:
+        q, k, v = tuple(torch.empty(shape, dtype=F16, device=qkv.device) for _ in range(3))
     capi.check(lib.esmc_qk_rope(qkv.data_ptr(), _dev(q_ln, "q_ln", torch.float32).data_ptr(),
                                 _dev(k_ln, "k_ln", torch.float32).data_ptr(), float(eps), q.data_ptr(), k.data_ptr(),
                                 v.data_ptr(), B, L, n_heads, 64, float(base), capi.stream_ptr()))
@@ -161,8 +176,11 @@ def esmc_attention(q, k, v, sequence_id=None, scale: float | None = None, out=No
     B, H, L, hd = q.shape
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _dev(t, n, F16)
-    sid = None if sequence_id is None else _dev(sequence_id, "sequence_id", torch.int32)
-    o = torch.empty(B, L, H * hd, dtype=F16, device=q.device) if out is None else _dev(out, "out", F16)
+    for t, n in ((k, "k"), (v, "v")):
+        if tuple(t.shape) != tuple(q.shape):
+            raise capi.EsmError(-2, f"esmc_attention: {n} {tuple(t.shape)} differs from q {tuple(q.shape)}")
+    sid = None if sequence_id is None else _out(sequence_id, "sequence_id", torch.int32, B * L)
+    o = torch.empty(B, L, H * hd, dtype=F16, device=q.device) if out is None else _out(out, "out", F16, B * L * H * hd)
     capi.check(lib.esmc_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(sid), o.data_ptr(), B, L, H, hd,
                                   float(hd ** -0.5 if scale is None else scale), capi.stream_ptr()))
     return o
@@ -173,7 +191,8 @@ def esmc_swiglu(x12, out=None):
     lib = capi.lib()
     _dev(x12, "x12", F16)
     M, F2 = x12.shape[0] if x12.dim() == 2 else x12.numel() // x12.shape[-1], x12.shape[-1]
-    y = torch.empty(*x12.shape[:-1], F2 // 2, dtype=F16, device=x12.device) if out is None else _dev(out, "out", F16)
+    y = (torch.empty(*x12.shape[:-1], F2 // 2, dtype=F16, device=x12.device) if out is None
+         else _out(out, "out", F16, M * (F2 // 2)))
     capi.check(lib.esmc_swiglu(x12.data_ptr(), y.data_ptr(), M, F2 // 2, capi.stream_ptr()))
     return y
 
@@ -181,10 +200,10 @@ def esmc_swiglu(x12, out=None):
 def parcae_step(z, z_init, refined, ln_w, ln_b, eps, a, b_mat, out=None):
     """a * z + LN(z_init + refined) @ B^T: z, z_init, refined [B, L, L, C] fp32; b_mat [C, C] fp16."""
     lib = capi.lib()
-    for t, n in ((z, "z"), (z_init, "z_init"), (refined, "refined")):
-        _dev(t, n, torch.float32)
     B, L, _, C = z.shape
-    out = torch.empty_like(z) if out is None else _dev(out, "out", torch.float32)
+    for t, n in ((z, "z"), (z_init, "z_init"), (refined, "refined")):
+        _out(t, n, torch.float32, z.numel())
+    out = torch.empty_like(z) if out is None else _out(out, "out", torch.float32, z.numel())
     capi.check(lib.parcae_step(z.data_ptr(), z_init.data_ptr(), refined.data_ptr(),
                                _dev(ln_w, "ln_w", torch.float32).data_ptr(), _dev(ln_b, "ln_b", torch.float32).data_ptr(),
                                float(eps), _dev(a, "a", torch.float32).data_ptr(), _dev(b_mat, "b_mat", F16).data_ptr(),
@@ -198,7 +217,8 @@ def expected_distance(r, w, bias, centers, out=None):
     _dev(r, "r", torch.float32)
     B, L, _, C = r.shape
     nb = w.shape[0]
-    ed = torch.empty(B, L, L, dtype=torch.float32, device=r.device) if out is None else _dev(out, "out", torch.float32)
+    ed = (torch.empty(B, L, L, dtype=torch.float32, device=r.device) if out is None
+          else _out(out, "out", torch.float32, B * L * L))
     capi.check(lib.distogram_expected_distance(r.data_ptr(), _dev(w, "w", F16).data_ptr(),
                                                _dev(bias, "bias", torch.float32).data_ptr(),
                                                _dev(centers, "centers", torch.float32).data_ptr(), ed.data_ptr(), B, L,
@@ -214,7 +234,7 @@ def abs_diff_quantile(x, y=None, q: float = 0.95, out=None):
         _dev(y, "y", torch.float32)
         if y.numel() != x.numel():
             raise capi.EsmError(-2, "abs_diff_quantile: x and y differ in size")
-    out = torch.empty(1, dtype=torch.float32, device=x.device) if out is None else _dev(out, "out", torch.float32)
+    out = torch.empty(1, dtype=torch.float32, device=x.device) if out is None else _out(out, "out", torch.float32, 1)
     capi.check(lib.abs_diff_quantile(x.data_ptr(), _ptr(y), x.numel(), float(q), out.data_ptr(), capi.stream_ptr()))
     return out
 
@@ -300,7 +320,7 @@ def q8_linear(x, q, s, b, group: int = 64, out=None, workspace=None, packed=None
     N = q.shape[0]
     if q.shape[1] != K or s.shape != (N, K // group) or b.shape != s.shape:
         raise capi.EsmError(-2, f"q8_linear: shapes x{tuple(x.shape)} q{tuple(q.shape)} s{tuple(s.shape)}")
-    y = torch.empty(M, N, dtype=F16, device=x.device) if out is None else _dev(out, "out", F16)
+    y = torch.empty(M, N, dtype=F16, device=x.device) if out is None else _out(out, "out", F16, M * N)
     if workspace is None:
         wp, wn = None, 0
     else:
@@ -316,6 +336,20 @@ def q8_linear(x, q, s, b, group: int = 64, out=None, workspace=None, packed=None
     capi.check(lib.q8_linear_ws(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), sbp, y.data_ptr(), M, K, N,
                                 group, wp, wn, capi.stream_ptr()))
     return y
+
+
+def q8_quantize(w, group: int = 64):
+    """MLX's affine 8-bit quantisation of fp32 W [N, K] along K (mx.quantize(W, 64, 8) with fp16
+    scales and biases, mlx_esmc.py:73-74) -> (q uint8 [N, K], s, b fp16 [N, K/64])."""
+    lib = capi.lib()
+    _dev(w, "w", torch.float32)
+    N, K = w.shape
+    q = torch.empty(N, K, dtype=torch.uint8, device=w.device)
+    s = torch.empty(N, K // group, dtype=F16, device=w.device)
+    b = torch.empty_like(s)
+    capi.check(lib.q8_quantize(w.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), N, K, group,
+                               capi.stream_ptr()))
+    return q, s, b
 
 
 def q8_dequant(q, s, b, group: int = 64):

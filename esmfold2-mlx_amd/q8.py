@@ -8,7 +8,8 @@ input axis of torch's [out, in] layout with fp16 scales and biases
 computes y = x . W^T with W = s*q + b on the gfx950 kernel: fp16 activations,
 fp32 accumulation, fp16 output. The scales and biases are packed once per layer
 into the kernel's per-tile layout, and shapes whose output tiles cannot fill the
-GPU get a per-M workspace (allocated once) so K is split over more workgroups.
+GPU split K over more workgroups through the device's shared scratch (one buffer
+for every layer, sized for the largest call).
 """
 
 from __future__ import annotations
@@ -16,7 +17,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import kernels
+from . import kernels, scratch
 
 GROUP = 64
 
@@ -33,7 +34,15 @@ class Q8Linear(nn.Module):
         self.register_buffer("biases", biases.detach().to(device=dev, dtype=torch.float16).contiguous())
         self.in_features, self.out_features = K, N
         self.register_buffer("packed", kernels.q8_pack_scales(self.scales, self.biases, GROUP))
-        self._ws = {}  # rows M -> split-K workspace (None: the shape runs unsplit)
+
+    @classmethod
+    def from_float(cls, w: torch.Tensor, **kw) -> "Q8Linear":
+        """Quantised from fp32 weights [N, K] (torch's [out, in] layout) on the GPU, as the
+        reference's layer_params quantises each linear from fp32 (mlx_esmc.py:70-74)."""
+        dev = kw.get("device")
+        dev = torch.device(dev) if dev is not None else torch.device("cuda", torch.cuda.current_device())
+        q, s, b = kernels.q8_quantize(w.detach().to(device=dev, dtype=torch.float32).contiguous(), GROUP)
+        return cls(q, s, b, **kw)
 
     @classmethod
     def from_packed_u32(cls, w_u32: torch.Tensor, scales, biases, **kw) -> "Q8Linear":
@@ -51,21 +60,19 @@ class Q8Linear(nn.Module):
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
         M = x2.shape[0]
-        if M not in self._ws:
-            self._ws[M] = kernels.q8_workspace(M, self.in_features, self.out_features, device=x2.device)
-        y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP, workspace=self._ws[M], packed=self.packed)
+        n = kernels.q8_workspace_bytes(M, self.in_features, self.out_features)
+        ws = scratch.get(n, x2.device) if n else None  # split-K partials, only while this call runs
+        y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP, workspace=ws, packed=self.packed)
         y = y.reshape(*lead, self.out_features)
         return y if x.dtype == torch.float16 else y.to(x.dtype)
 
     def partials(self, x: torch.Tensor):
         """(partials [splits, M, N] fp32, splits) of x . W^T for a consumer that sums them in split
         order (``kernels.esmc_layer_norm(..., y_parts=...)``): rounded to fp16, the sum is
-        ``forward(x)`` bit for bit. The view lives in this layer's per-M buffer (the split-K
-        workspace when the shape splits), valid until the layer's next call."""
+        ``forward(x)`` bit for bit. The view lives in the device's shared scratch: valid for work
+        queued after this call on the same stream until the next call of any module that uses
+        the scratch."""
         x2 = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
         M = x2.shape[0]
-        need = kernels.q8_partials_bytes(M, self.in_features, self.out_features) + 256
-        buf = self._ws.get(M)
-        if buf is None or buf.numel() < need:
-            buf = self._ws[M] = torch.empty(need, dtype=torch.uint8, device=x2.device)
+        buf = scratch.get(kernels.q8_partials_bytes(M, self.in_features, self.out_features), x2.device)
         return kernels.q8_linear_partials(x2, self.q, self.scales, self.biases, buf, GROUP, packed=self.packed)

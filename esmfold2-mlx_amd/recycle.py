@@ -74,6 +74,7 @@ class ParcaeLoop:
         self.p, self.threshold, self.source = lm_dropout, threshold, source
         self.min_steps, self.burn_rng = min_steps, burn_rng
         self.steps_run, self.history = 0, []
+        self.exit_out = None  # on an early exit with source "coda": coda(readout(z)) of the exit step
 
     @classmethod
     def from_model(cls, model, **kw) -> "ParcaeLoop":
@@ -100,10 +101,12 @@ class ParcaeLoop:
         return torch.matmul(z, self.readout_w.T)
 
     def exit_distance(self, z, mask=None):
+        """(expected distance per pair, the coda output or None) if the loop stopped at z."""
         r = self.readout(z)
         if self.source == "coda":
             r = self.coda(r, mask)
-        return self.signal.expected_distance(r)
+            return self.signal.expected_distance(r), r
+        return self.signal.expected_distance(r), None
 
     def run(self, z, z_init, lm_z, pair_mask, a, b_mat, total_steps: int, dropout=None):
         """The loop; ``dropout(lm_z, p)`` defaults to torch's F.dropout(training=True)."""
@@ -115,6 +118,7 @@ class ParcaeLoop:
         a = a.float().expand(z.shape[-1]).contiguous() if a.numel() == 1 else a.float().contiguous()
         b16 = b_mat.to(F16).contiguous()
         self.history, self.steps_run, prev = [], 0, None
+        self.exit_out = None
         adaptive = self.threshold is not None
         for k in range(1, total_steps + 1):
             lm_z_i = drop(lm_z, self.p)
@@ -122,7 +126,7 @@ class ParcaeLoop:
             self.steps_run = k
             if not adaptive or k < self.min_steps - 1 or k == total_steps:
                 continue
-            ed = self.exit_distance(z, mask)
+            ed, out = self.exit_distance(z, mask)
             if k >= self.min_steps and prev is not None:
                 d = DistogramSignal.p95_change(ed, prev)
                 self.history.append({f"{self.source}_p95": d})
@@ -130,6 +134,7 @@ class ParcaeLoop:
                     if self.burn_rng:
                         for _ in range(total_steps - k):
                             drop(lm_z, self.p)
+                    self.exit_out = out
                     return z
             prev = ed
         return z

@@ -22,7 +22,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import capi
+from . import capi, scratch
 
 F16 = torch.float16
 
@@ -52,7 +52,6 @@ class TriMul(nn.Module):
         self.outgoing = bool(outgoing)
         self.ln_in_eps, self.ln_mix_eps = float(ln_in_eps), float(ln_mix_eps)
         self.out_mask = bool(out_mask)
-        self._ws = {}
 
     # --- construction from the reference's module ------------------------------------------
     @classmethod
@@ -83,21 +82,17 @@ class TriMul(nn.Module):
 
     # --- forward -----------------------------------------------------------------------------
     def workspace(self, B: int, L: int, device) -> torch.Tensor:
-        key = (device, B, L)
-        ws = self._ws.get(key)
-        if ws is None:
-            nbytes = capi.lib().tmu_workspace_bytes(B, L, self.c)
-            ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
-            self._ws = {key: ws}  # one shape at a time: the previous one is released
-        return ws
+        """The a, b, x planes of one call: a 256-byte aligned view of the device's shared scratch
+        (every update of a trunk runs in the same bytes, one after another)."""
+        return scratch.get(capi.lib().tmu_workspace_bytes(B, L, self.c), device)
 
     def run(self, z16: torch.Tensor, mask16: torch.Tensor | None, out: torch.Tensor, residual: bool) -> torch.Tensor:
         """fp16 in/out on the current stream; ``out`` may be ``z16`` itself when ``residual``."""
         lib = capi.lib()
         B, L, _, C = z16.shape
-        ws = self.workspace(B, L, z16.device)
-        base = ws.data_ptr()
-        base = (base + 255) // 256 * 256
+        if tuple(out.shape) != tuple(z16.shape) or out.dtype != F16 or not out.is_contiguous():
+            raise capi.EsmError(-2, f"out must be a contiguous fp16 {tuple(z16.shape)} tensor")
+        base = self.workspace(B, L, z16.device).data_ptr()
         capi.check(lib.tmu_forward(z16.data_ptr(), None if mask16 is None else mask16.data_ptr(),
                                    self.ln_in_w.data_ptr(), self.ln_in_b.data_ptr(), self.ln_in_eps,
                                    self.w_bundle.data_ptr(), self.ln_mix_w.data_ptr(), self.ln_mix_b.data_ptr(),
@@ -140,6 +135,9 @@ class TriMulPair(nn.Module):
 
     def forward(self, z: torch.Tensor, mask: torch.Tensor | None = None, out: torch.Tensor | None = None):
         z16, m16 = prepare(z, mask, self.t_out.C)
+        if out is not None and (tuple(out.shape) != tuple(z16.shape) or out.dtype != F16 or not out.is_cuda
+                                or not out.is_contiguous()):
+            raise capi.EsmError(-2, f"out must be a contiguous fp16 device tensor of shape {tuple(z16.shape)}")
         z1 = torch.empty_like(z16) if out is None else out
         self.t_out.run(z16, m16, z1, residual=True)
         self.t_in.run(z1, m16, z1, residual=True)

@@ -21,7 +21,7 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
-from . import capi, kernels
+from . import capi, kernels, scratch
 from .trimul import TriMul, prepare
 
 F16 = torch.float16
@@ -104,6 +104,7 @@ class _Graph:
     graph: torch.cuda.CUDAGraph
     z: torch.Tensor
     mask: torch.Tensor | None
+    scratch: torch.Tensor | None  # the shared scratch the captured launches use, kept alive
 
 
 class PairTrunk(nn.Module):
@@ -168,5 +169,5 @@ class PairTrunk(nn.Module):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 self.run_(z16, m16, recycles)
-            self._graph = _Graph(key, g, z16, m16)
+            self._graph = _Graph(key, g, z16, m16, scratch.current(z16.device))
         return self._graph.graph.replay

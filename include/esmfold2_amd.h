@@ -46,6 +46,10 @@ const char* esm_last_error(void);
 /* Library version string and the device architecture it was built for. */
 const char* esm_version(void);
 
+/* sha256 (hex) over the sources and headers the library was compiled from; a loader
+ * compares it with the current sources to refuse or rebuild a stale library. */
+const char* esm_source_hash(void);
+
 /* Bytes of caller-provided workspace tmu_forward needs for B x L x L cells with
  * c latent channels: two operands [B, c, L, ld] and the contraction output
  * [B, c, L, ld], fp16, with ld = tmu_leading_dim(L). */
@@ -95,7 +99,7 @@ int tmu_project(const esm_half* z, const esm_half* mask, const float* ln_w, cons
  * x     [batch, L, ldx] fp16; columns [L, ldx) are written with zeros.
  * scale fp32 factor applied to the fp32 accumulator before the one rounding to
  *       fp16 (the fp16 scheme uses 1/256, mlx_trunk.py:14-19, :47-48).
- * ld % 8 == 0, ld >= L; ldx % 8 == 0, ldx >= L. Pointers 16-byte aligned.
+ * ld % 8 == 0, ld >= L; ldx % 8 == 0, L <= ldx <= roundup(L, 64). Pointers 16-byte aligned.
  */
 int tmu_contract(const esm_half* a, const esm_half* b, esm_half* x, int batch, int L, int ld, int ldx, float scale,
                  void* stream);
@@ -283,6 +287,24 @@ int parcae_step(const float* z, const float* z_init, const float* refined, const
 int distogram_expected_distance(const float* r, const esm_half* w, const float* bias, const float* centers, float* ed,
                                 int B, int L, int C, int nbins, void* stream);
 int abs_diff_quantile(const float* x, const float* y, size_t n, float q, float* out, void* stream);
+
+/*
+ * Quantise fp32 weights to the 8-bit layout q8_linear reads: MLX's affine scheme, group
+ * 64 along K, scales and biases rounded to fp16.
+ *
+ * Replaces, in the reference:
+ *   wq, scales, biases = mx.quantize(W, group_size=64, bits=8)   mlx_esmc.py:73
+ *   scales.astype(mx.float16), biases.astype(mx.float16)         mlx_esmc.py:74
+ *
+ * Per group of 64 (fp32 arithmetic, IEEE division, rint = round half to even):
+ *   scale = max((max - min) / 255, 1e-7), negated unless |min| > |max|;
+ *   edge = min if |min| > |max| else max;  q0 = rint(edge / scale);
+ *   q0 != 0: scale = edge / q0, bias = edge;  q0 == 0: bias = 0;
+ *   q = clamp(rint((w - bias) / scale), 0, 255).
+ * w [N, K] fp32 (torch's [out, in] layout), 16-byte aligned; q [N, K] uint8 (4-byte
+ * aligned); s, b [N, K/64] fp16. group = 64, K % 64 == 0.
+ */
+int q8_quantize(const float* w, uint8_t* q, esm_half* s, esm_half* b, int N, int K, int group, void* stream);
 
 /*
  * Dequantise only: w[n, k] = RN_fp16(s[n, k/group] * q[n, k] + b[n, k/group]),

@@ -14,6 +14,16 @@ Reference arithmetic restated here (paths relative to the reference repo):
    codes are packed four per uint32, little-endian, i.e. byte-identical to a
    row-major uint8 [N, K] array, which is the layout used here.)
 
+  mlx_esmc.py:70-74       layer_params quantises each linear from fp32 with
+                          mx.quantize(W, group_size=64, bits=8), then casts scales and
+                          biases to fp16. mx.quantize's affine scheme (mlx 0.32.3,
+                          affine_quantize in mlx/ops.cpp; its published algorithm, restated
+                          in ``quantize_affine``): per group, scale = max((max - min)/255,
+                          1e-7), signed towards the larger-magnitude extreme ("edge"),
+                          q0 = round(edge / scale); unless q0 = 0 the scale becomes
+                          edge / q0 and the bias edge (so 0 is on the grid), else bias 0;
+                          codes clip(round((w - bias) / scale), 0, 255), round half to even.
+
 Pinned by (tests/test_oracle_q8.py):
   * exactness argument: s*q is exact in fp32 and fp64 (11 + 8 significant bits) and
     the fp64 sum s*q + b is exact at these magnitudes, so dequant_exact is the real
@@ -21,7 +31,14 @@ Pinned by (tests/test_oracle_q8.py):
     against fractions.Fraction arithmetic on random codes;
   * special cases: q = 0 gives b, s = 0 gives b, q = 255 with b = 0 gives s*255;
   * the GEMM against a pure-Python loop on tiny shapes, and against the
-    dequantise-then-matmul identity y = sum_g s_g (x_g . q_g) + b_g sum(x_g).
+    dequantise-then-matmul identity y = sum_g s_g (x_g . q_g) + b_g sum(x_g);
+  * quantize_affine by hand-computed groups (a ramp from -1 to 0.5, its mirror, a
+    constant group, an all-zero group) and by what the scheme fixes for every group:
+    codes in 0..255, the edge element at code 0, the other extreme at code 255 up to the
+    rescale, |s*q + b - w| <= |s|/2 with the fp32 parameters, and 0 exactly on the grid.
+    MLX's own GPU kernel may differ in rounding details (its round, its division): that
+    exact choice is parity unpinned, as no MLX is installed and the reference holds no
+    quantised vectors.
 """
 
 from __future__ import annotations
@@ -30,6 +47,36 @@ import numpy as np
 import torch
 
 GROUP = 64  # mlx_esmc.py:43
+
+
+def quantize_affine(w: np.ndarray, group: int = GROUP, bits: int = 8):
+    """(codes uint8 [N, K], scales fp32 [N, K/group], biases fp32): mx.quantize's affine scheme,
+    restated in fp32 with IEEE division and round-half-to-even (mlx_esmc.py:73)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    N, K = w.shape
+    assert K % group == 0
+    f = np.float32
+    g = w.reshape(N, K // group, group)
+    w_max, w_min = g.max(-1), g.min(-1)
+    n_bins = f((1 << bits) - 1)
+    mask = np.abs(w_min) > np.abs(w_max)
+    scale = np.maximum((w_max - w_min) / n_bins, f(1e-7)).astype(f)
+    scale = np.where(mask, scale, -scale).astype(f)
+    edge = np.where(mask, w_min, w_max).astype(f)
+    q0 = np.rint(edge / scale).astype(f)
+    at_zero = q0 == 0
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scale = np.where(at_zero, scale, edge / np.where(at_zero, f(1), q0)).astype(f)
+    bias = np.where(at_zero, f(0), edge).astype(f)
+    q = np.clip(np.rint((g - bias[..., None]) / scale[..., None]), 0, n_bins).astype(np.uint8)
+    return q.reshape(N, K), scale, bias
+
+
+def quantize_f16(w: np.ndarray, group: int = GROUP):
+    """quantize_affine with the scales and biases cast to fp16, as layer_params stores them
+    (mlx_esmc.py:74): the (q, s, b) arrays of an 8-bit layer."""
+    q, s, b = quantize_affine(w, group)
+    return q, s.astype(np.float16), b.astype(np.float16)
 
 
 def dequant_exact(q: np.ndarray, s: np.ndarray, b: np.ndarray, group: int = GROUP) -> np.ndarray:

@@ -162,6 +162,53 @@ def trimul_pair(z, mask, p_out: TriMulWeights, p_in: TriMulWeights):
     return z1 + trimul(z1, mask, p_in, False)
 
 
+CONTRACT_SCALE = 256.0  # mlx_trunk.py:33
+
+
+def rn16(t: torch.Tensor) -> torch.Tensor:
+    """Round to fp16 and back to the working dtype (one storage rounding)."""
+    return t.to(torch.float16).to(t.dtype)
+
+
+def trimul_fp16ref(z: torch.Tensor, mask: torch.Tensor | None, p: TriMulWeights,
+                   outgoing: bool | None = None) -> torch.Tensor:
+    """z + update with the reference's fp16 storage at every op output: the arithmetic of
+    the fp16 MLX trunk with its Metal kernels (mlx_trunk_kernels.py:210-229, weights from
+    mlx_trunk.py:40-55 with dtype fp16), computed in fp32 with one fp16 rounding per stored
+    tensor. Used to measure how far the reference's own fp16 scheme sits from exact
+    arithmetic, the floor any fp16 implementation is compared against.
+
+      weights   fp16; w_in[:, :c] (s_a) pre-divided by 256 (mlx_trunk.py:46-48)
+      n         RN(LN_in(z))                                  (mlx_trunk_kernels.py:233)
+      proj      RN(n @ w_in)                                  (:214)
+      a, b      RN(s * sigmoid(g) * m), fp32 inside           (gate_cf, :60-64)
+      x         RN(a @ b^T)  (incoming: a^T @ b)              (:219)
+      mixed     RN(RN(LN_mix(x, eps / 256^2)) @ w_emit)       (ln_cf_to_cl :107-147, :224)
+      g         RN(n @ w_out_gate)                            (:225)
+      z'        RN(z + mixed * sigmoid(g)), fp32 inside       (resgate_ln, :165-190)
+    ``z`` holds fp16-representable values in fp32 (or fp64)."""
+    if outgoing is None:
+        outgoing = p.outgoing
+    f32 = torch.float32
+    c = p.c
+    w = p.w_bundle.to(f32).clone()
+    w[:c] /= CONTRACT_SCALE
+    w, we, wg = rn16(w), rn16(p.w_emit.to(f32)), rn16(p.w_gate.to(f32))
+    g16 = lambda t: rn16(t.to(f32))  # noqa: E731  (LN parameters are stored fp16 too)
+    zf = z.to(f32)
+    n = rn16(layer_norm(zf, g16(p.ln_in_w), g16(p.ln_in_b), p.ln_in_eps))
+    proj = rn16(F.linear(n, w))
+    routed = proj[..., :2 * c] * torch.sigmoid(proj[..., 2 * c:])
+    if mask is not None:
+        routed = routed * mask.to(f32).unsqueeze(-1)
+    routed = rn16(routed)
+    x = rn16(contract(routed[..., :c], routed[..., c:], outgoing))
+    mix_eps = p.ln_mix_eps / CONTRACT_SCALE ** 2
+    mixed = rn16(F.linear(rn16(layer_norm(x, g16(p.ln_mix_w), g16(p.ln_mix_b), mix_eps)), we))
+    g = rn16(F.linear(n, wg))
+    return rn16(zf + mixed * torch.sigmoid(g)).to(z.dtype)
+
+
 def make_pair_inputs(L: int, C: int, c: int, seed: int = 0, dtype=torch.float16, B: int = 1,
                      pad_from: int | None = None):
     """Seeded inputs of a TMU pair: z [B,L,L,C] ~ N(0,1), then T_out's and T_in's weights.

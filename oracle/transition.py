@@ -93,3 +93,33 @@ def stack_forward(z, mask, blocks, recycles: int = 1, store=None):
         for blk in blocks:
             z = block_forward(z, mask, blk, store)
     return z
+
+
+def transition_fp16ref(z: torch.Tensor, p: TransitionWeights) -> torch.Tensor:
+    """The transition with the reference's fp16 storage (mlx_trunk_kernels.py:246-249):
+    h = RN(LN(z)); u = RN(h @ W1^T) (SwiGLU: s = RN(silu(x1) * x2), fp32 inside, with
+    x = RN(h @ [W1; W2]^T)); z' = RN(z + u @ W3^T) in one rounding (mx.addmm). fp16
+    weights, fp32 arithmetic."""
+    f32 = torch.float32
+    r = lambda t: t.to(torch.float16).to(f32)  # noqa: E731
+    zf = z.to(f32)
+    h = r(layer_norm(zf, r(p.ln_w.to(f32)), r(p.ln_b.to(f32)), p.eps))
+    u = r(F.linear(h, r(p.w1.to(f32))))
+    if p.swiglu:
+        u = r(F.silu(u) * r(F.linear(h, r(p.w2.to(f32)))))
+    else:
+        u = torch.relu(u)
+    return r(zf + F.linear(u, r(p.w3.to(f32)))).to(z.dtype)
+
+
+def stack_forward_fp16ref(z, mask, blocks, recycles: int = 1):
+    """The block stack with the reference's fp16 storage at every op output
+    (``tmu.trimul_fp16ref``, ``transition_fp16ref``): the error floor of the reference's
+    own fp16 trunk, for comparison with exact arithmetic."""
+    from .tmu import trimul_fp16ref
+    for _ in range(recycles):
+        for blk in blocks:
+            z = trimul_fp16ref(z, mask, blk.tri_out, True)
+            z = trimul_fp16ref(z, mask, blk.tri_in, False)
+            z = transition_fp16ref(z, blk.trans)
+    return z

@@ -107,9 +107,19 @@ def test_rejects_null_and_bad_shapes(lib):
     fake = ctypes.c_void_p(4096)
     assert lib.tmu_contract(fake, fake, fake, 1, 10, 12, 16, 1.0, None) == -2
     assert "multiples of 8" in _err(lib)
+    # x columns past roundup(L, 64) would never be written: refused
+    assert lib.tmu_contract(fake, fake, fake, 1, 8, 8, 136, 1.0, None) == -2
+    assert "ldx <= 64" in _err(lib)
     # misaligned pointers
     odd = ctypes.c_void_p(4096 + 2)
     assert lib.tmu_contract(odd, fake, fake, 1, 10, 16, 16, 1.0, None) == -3
+
+
+def test_library_matches_its_sources(pkg):
+    # the in-tree library carries the content hash of the sources it was compiled from
+    lib = pkg.capi.lib(require_gpu=False)
+    assert lib.esm_source_hash().decode() == pkg.build.source_hash() == pkg.build.library_hash()
+    assert pkg.build.up_to_date()
 
 
 def test_empty_inputs_are_a_no_op(lib):

@@ -200,3 +200,63 @@ def test_hip_esmc_hidden_states_and_cache(gpu_lib, pkg, tmp_path):
     again = pkg.esmc.HipEsmc.from_cache(path, n_heads=H)
     hs2 = again(input_ids=ids.to(DEV), sequence_id=sid.to(DEV)).hidden_states
     assert torch.equal(hs, hs2)
+
+
+def test_hip_esmc_from_hf_weights(gpu_lib, pkg, tmp_path):
+    # the product quantiser: HF-named fp32 tensors -> 8-bit layers (wqkv = [q; k; v], w1 = [gate; up],
+    # group 64 along in, fp16 scales and biases) -> the cache layout, as the reference's
+    # layer_params / from_shards (mlx_esmc.py:53-75, :116-137)
+    from oracle import q8 as oq8
+    D, F_, H, n = 128, 256, 2, 2
+    g = _gen(21)
+    hf = {"esmc.embed_tokens.weight": torch.randn(33, D, generator=g),
+          "esmc.norm.weight": 1 + 0.1 * torch.randn(D, generator=g)}
+    shapes = {"self_attn.q_proj.weight": (D, D), "self_attn.k_proj.weight": (D, D), "self_attn.v_proj.weight": (D, D),
+              "self_attn.o_proj.weight": (D, D), "mlp.gate_proj.weight": (F_, D), "mlp.up_proj.weight": (F_, D),
+              "mlp.down_proj.weight": (D, F_)}
+    for i in range(n):
+        for name, shp in shapes.items():
+            hf[f"esmc.layers.{i}.{name}"] = torch.randn(*shp, generator=g) * shp[1] ** -0.5
+        for name in ("input_layernorm", "post_attention_layernorm"):
+            hf[f"esmc.layers.{i}.{name}.weight"] = 1 + 0.1 * torch.randn(D, generator=g)
+            hf[f"esmc.layers.{i}.{name}.bias"] = 0.1 * torch.randn(D, generator=g)
+        for name in ("q_norm", "k_norm"):
+            hf[f"esmc.layers.{i}.self_attn.{name}.weight"] = 1 + 0.1 * torch.randn(D, generator=g)
+    path = tmp_path / "cache" / "esmc_q8.safetensors"
+    model = pkg.esmc.HipEsmc.from_hf(hf, n_heads=H, cache=path)
+    assert len(model.layers) == n and path.exists()
+    # the row layout of the fused linears and the quantised arrays, against the oracle's quantiser
+    for i, blk in enumerate(model.layers):
+        for lin, parts in (("wqkv", ("q_proj", "k_proj", "v_proj")), ("w1", ("gate_proj", "up_proj"))):
+            pre = "self_attn" if lin == "wqkv" else "mlp"
+            w = torch.cat([hf[f"esmc.layers.{i}.{pre}.{p}.weight"] for p in parts]).numpy()
+            qr, sr, br = oq8.quantize_f16(w)
+            m = getattr(blk, lin)
+            assert np.array_equal(m.q.cpu().numpy(), qr)
+            assert np.array_equal(m.scales.cpu().numpy().view(np.uint16), sr.view(np.uint16))
+            assert np.array_equal(m.biases.cpu().numpy().view(np.uint16), br.view(np.uint16))
+    # hidden states against the oracle blocks built from the oracle's quantisation
+    ps = []
+    for i in range(n):
+        lw = lambda nm: hf[f"esmc.layers.{i}.{nm}"]  # noqa: E731
+        qw = {}
+        for lin, names in (("wqkv", ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight")),
+                           ("wo", ("self_attn.o_proj.weight",)), ("w1", ("mlp.gate_proj.weight", "mlp.up_proj.weight")),
+                           ("w2", ("mlp.down_proj.weight",))):
+            qw[lin] = oe.Q8Weights(*oq8.quantize_f16(torch.cat([lw(nm) for nm in names]).numpy()))
+        ps.append(oe.EsmcBlockWeights(lw("input_layernorm.weight"), lw("input_layernorm.bias"),
+                                      lw("self_attn.q_norm.weight"), lw("self_attn.k_norm.weight"),
+                                      lw("post_attention_layernorm.weight"), lw("post_attention_layernorm.bias"),
+                                      qw["wqkv"], qw["wo"], qw["w1"], qw["w2"]))
+    ids = torch.randint(0, 33, (1, 40), generator=g)
+    hs = model(input_ids=ids.to(DEV)).hidden_states
+    x = hf["esmc.embed_tokens.weight"].double()[ids]
+    rs = math.sqrt(n / 36)
+    for i, p in enumerate(ps):
+        assert float((hs[i].double().cpu() - x).abs().max()) <= 1e-2 * float(x.pow(2).mean().sqrt()) + 1e-6
+        x = oe.block_forward(p, x, None, n_heads=H, res_scale=rs, weights="f16")
+    last = F.layer_norm(x, (D,), hf["esmc.norm.weight"].double(), None, 1e-5)
+    assert float((hs[n].double().cpu() - last).abs().max()) <= 1e-2 * float(last.pow(2).mean().sqrt())
+    # the cache written on conversion loads back (from_hf finds it) with the same hidden states
+    again = pkg.esmc.HipEsmc.from_hf({}, n_heads=H, cache=path)
+    assert torch.equal(again(input_ids=ids.to(DEV)).hidden_states, hs)

@@ -119,14 +119,35 @@ def test_q8_workspace_sizes_and_errors(gpu_lib, pkg):
 
 
 def test_q8_module_split_k_workspace(gpu_lib, pkg):
-    # the module keeps one workspace per row count and reuses it
+    # the split-K partials run in the device's shared scratch
     x, q, s, b = q8.make_q8_inputs(238, 4096, 640, seed=9)
     lin = pkg.q8.Q8Linear(torch.from_numpy(q), torch.from_numpy(s), torch.from_numpy(b))
     xt = torch.from_numpy(x).to(DEV)
+    assert pkg.kernels.q8_workspace_bytes(238, 4096, 640) > 0
     y = lin(xt)
-    assert lin._ws[238] is not None
+    assert pkg.scratch.reserved(DEV) >= pkg.kernels.q8_workspace_bytes(238, 4096, 640)
     _check(y.cpu().numpy(), x, q, s, b)
     _check(lin(xt).cpu().numpy(), x, q, s, b)
+
+
+def test_q8_memory_stops_growing_over_row_counts(gpu_lib, pkg):
+    # many layers and many sequence lengths share one scratch buffer: device memory stays
+    # flat once the largest shape has run, and results are unchanged by the sharing
+    K, N = 4096, 640
+    layers = [pkg.q8.Q8Linear(*(torch.from_numpy(a) for a in q8.make_q8_inputs(8, K, N, seed=40 + i)[1:]))
+              for i in range(4)]
+    xs = {M: torch.from_numpy(q8.make_q8_inputs(M, K, N, seed=M)[0]).to(DEV) for M in (256, 31, 97, 200, 5)}
+    first = {M: [lin(x) for lin in layers] for M, x in xs.items()}
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    for rnd in range(3):
+        for M, x in xs.items():
+            for lin, y0 in zip(layers, first[M]):
+                assert torch.equal(lin(x).view(torch.int16), y0.view(torch.int16))
+        torch.cuda.synchronize()
+        assert torch.cuda.memory_allocated() <= base, f"round {rnd}: {torch.cuda.memory_allocated()} > {base}"
+    _check(first[97][2].cpu().numpy(), *q8.make_q8_inputs(97, K, N, seed=97)[:1],
+           *q8.make_q8_inputs(8, K, N, seed=42)[1:])
 
 
 @pytest.mark.parametrize("M,K,N", [(238, 2560, 640), (238, 10240, 320), (7, 192, 192)])
@@ -147,3 +168,38 @@ def test_q8_packed_scales_same_bits(gpu_lib, pkg, M, K, N):
     y_packed = pkg.kernels.q8_linear(x, q, s, b, workspace=ws, packed=sb)
     assert torch.equal(y_plain.view(torch.int16), y_packed.view(torch.int16))
     _check(y_packed.cpu().numpy(), *q8.make_q8_inputs(M, K, N, seed=N))
+
+
+def _quant_cases():
+    rng = np.random.default_rng(7)
+    w = rng.standard_normal((96, 640)).astype(np.float32) * rng.uniform(0.01, 3, (96, 1)).astype(np.float32)
+    w[0, :64] = np.linspace(-1, 0.5, 64)          # hand-computed group: bias -1, step 1/170
+    w[1, :64] = 0.3                                # constant group: code 0, bias 0.3
+    w[2, :64] = 0.0                                # all-zero group: bias 0 (q0 = 0)
+    w[3] = np.abs(w[3])                            # all-positive groups
+    w[4] = -np.abs(w[4])                           # all-negative groups
+    w[5, 70] = 40.0                                # an outlier
+    w[6, :64] = rng.integers(-3, 4, 64) * 0.25     # ties at half steps
+    return w
+
+
+def test_quantize_matches_oracle_bit_exact(gpu_lib, pkg):
+    # the GPU quantiser (MLX's affine scheme, mlx_esmc.py:73-74) gives the oracle's codes, fp16
+    # scales and fp16 biases bit for bit; its dequantised weights sit within the scheme's bound
+    w = _quant_cases()
+    q, s, b = pkg.kernels.q8_quantize(_t(w))
+    qr, sr, br = q8.quantize_f16(w)
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(s.cpu().numpy().view(np.uint16), sr.view(np.uint16))
+    assert np.array_equal(b.cpu().numpy().view(np.uint16), br.view(np.uint16))
+    wd = pkg.kernels.q8_dequant(q, s, b).float().cpu().numpy()
+    step = np.repeat(np.abs(sr.astype(np.float32)), 64, axis=1)
+    assert np.all(np.abs(wd - w) <= 1.5 * step + 1e-3 * np.abs(w) + 1e-6)
+    # a larger layer, and the module built from fp32 weights computes with exactly these arrays
+    w2 = np.random.default_rng(8).standard_normal((640, 2560)).astype(np.float32) / 50
+    lin = pkg.q8.Q8Linear.from_float(torch.from_numpy(w2))
+    qr, sr, br = q8.quantize_f16(w2)
+    assert np.array_equal(lin.q.cpu().numpy(), qr)
+    assert np.array_equal(lin.scales.cpu().numpy().view(np.uint16), sr.view(np.uint16))
+    x = np.random.default_rng(9).standard_normal((238, 2560)).astype(np.float16)
+    _check(lin(_t(x)).cpu().numpy(), x, qr, sr, br)

@@ -8,9 +8,12 @@ Bars, on the accumulated update u = z_out - z_in: for one block (three ops), the
 triangle update's max|err| <= 1e-2 x RMS(u). Deeper stacks accumulate one op's error per
 residual add (each op sits near 3e-3 x RMS of its own update) and fp16 roundings of a
 growing z, where a single-ulp difference of the largest values (|z| up to 16 x RMS(u))
-already reaches 1e-2 x RMS(u): measured on the GPU at L=40, max|err| / RMS(u) is 5e-3
-after 1 block, 9e-3 after 8 and 1.4e-2 to 1.7e-2 after 8 blocks x 3 recycles, while the
-normwise error stays near 2e-3. For those the bar is normwise RMS(err) <= 1e-2 x RMS(u)
+already reaches 1e-2 x RMS(u). The reference's own fp16 scheme has the same floor: at the
+block-stack workload (L=238, 8 blocks x 3 recycles) the oracle with every op output
+stored in fp16 as the reference stores it (oracle.transition.stack_forward_fp16ref) sits
+at max 1.75e-2 x RMS(u) from fp64, and exact arithmetic with only the residual stream
+stored in fp16 at 1.66e-2 (tests/test_oracle_transition.py checks the floor at L=48).
+For stacks deeper than one block the bar is therefore normwise RMS(err) <= 1e-2 x RMS(u)
 plus max|err| <= 3e-2 x RMS(u).
 """
 
@@ -67,6 +70,53 @@ def test_stack_matches_oracle(gpu_lib, pkg, L, n_blocks, recycles, pad):
     ref = otr.stack_forward(z.double(), m64, _oracle_blocks(blocks), recycles)
     r64 = _check(z16.cpu(), z, ref, **bars)
     print(f"stack L={L} {n_blocks}x{recycles}: err/RMS {r16:.2e} (fp16 stream), {r64:.2e} (fp64 stream)")
+
+
+def test_block_stack_workload_full_size(gpu_lib, pkg):
+    # the block-stack workload at its own size: L=238, 8 blocks x (T_out, T_in, ReLU MLP
+    # 128->512->128) x 3 recycles with z carried, fp16, all-ones mask; eager launches and the
+    # HIP-graph replay the bench times give the same bits
+    L, nb, rc = 238, 8, 3
+    z, blocks = pkg.workloads.block_stack(L, n_blocks=nb, seed=0)
+    trunk = pkg.trunk.PairTrunk.from_weights(blocks)
+    z16 = z.to(DEV).contiguous()
+    trunk.run_(z16, None, rc)
+    zg = torch.empty_like(z16)
+    replay = trunk.graphed(zg, None, recycles=rc)
+    for _ in range(2):
+        zg.copy_(z.to(DEV))
+        replay()
+        torch.cuda.synchronize()
+        assert torch.equal(zg.view(torch.int16), z16.view(torch.int16))
+    got = z16.cpu()
+    assert torch.isfinite(got.float()).all()
+    with torch.no_grad():
+        ref = otr.stack_forward(z.double(), None, _oracle_blocks(blocks), rc)
+    r = _check(got, z, ref, bar=3e-2, norm_bar=1e-2)
+    print(f"block stack L={L} {nb}x{rc}: max|err|/RMS(u) {r:.3e} against fp64 "
+          f"(the reference's fp16 scheme: 1.75e-2)")
+
+
+def test_trunk_scratch_is_one_workspace(gpu_lib, pkg):
+    # a 24-block trunk at L=238 holds one TMU workspace (the device's shared scratch), not
+    # one per update; the bits equal a run whose blocks each start from a fresh buffer
+    L = 238
+    z, blocks = pkg.workloads.block_stack(L, n_blocks=24, seed=4)
+    trunk = pkg.trunk.PairTrunk.from_weights(blocks)
+    pkg.scratch.release(DEV)
+    zs = z.to(DEV).contiguous()
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    trunk.run_(zs, None)
+    torch.cuda.synchronize()
+    grown = torch.cuda.memory_allocated() - before
+    ws = pkg.kernels.workspace_bytes(1, L, 128)
+    assert ws <= grown <= ws + (1 << 20), f"grew {grown} bytes for a {ws}-byte workspace"
+    zf = z.to(DEV).contiguous()
+    for blk in trunk.blocks:
+        pkg.scratch.release(DEV)
+        blk.run_(zf, None)
+    assert torch.equal(zs.view(torch.int16), zf.view(torch.int16))
 
 
 def test_folding_trunk_drop_in_contract(gpu_lib, pkg):

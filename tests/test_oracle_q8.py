@@ -96,3 +96,60 @@ def test_f16_weight_rounding_is_within_the_gemm_tolerance(which):
     y, y16 = q8.q8_linear(x, q, s, b), q8.q8_linear(x, q, s, b, weights=which)
     rel = np.linalg.norm(y16 - y) / np.linalg.norm(y)
     assert 1e-5 < rel < 4e-4
+
+
+def test_quantize_affine_hand_computed_groups():
+    # a ramp from -1 to 0.5: |min| > |max|, so the edge is -1: scale 1.5/255 = 1/170 exactly
+    # representable as -1/-170 after the rescale (q0 = round(-170) = -170), bias -1;
+    # code k = round(255 k / 63)
+    w = np.linspace(-1, 0.5, 64, dtype=np.float32)
+    q, s, b = q8.quantize_affine(w[None])
+    assert b[0, 0] == np.float32(-1.0) and s[0, 0] == np.float32(-1.0) / np.float32(-170.0)
+    assert q[0, 0] == 0 and q[0, 1] == 4 and q[0, 4] == 16 and q[0, -1] == 255
+    # its mirror (from -0.5 up to 1): the edge is +1, the scale negative (-1/170), bias +1,
+    # code 0 at w = 1 (the last element), 255 at w = -0.5
+    q, s, b = q8.quantize_affine(-w[::-1][None].copy())
+    assert b[0, 0] == np.float32(1.0) and s[0, 0] == np.float32(1.0) / np.float32(-170.0)
+    assert q[0, -1] == 0 and q[0, 0] == 255 and q[0, -2] == 4
+    # a constant group is represented exactly by its bias with code 0; an all-zero group
+    # keeps bias 0 (q0 = 0) and the minimum scale magnitude 1e-7
+    q, s, b = q8.quantize_affine(np.full((1, 64), 0.3, np.float32))
+    assert np.all(q == 0) and b[0, 0] == np.float32(0.3)
+    q, s, b = q8.quantize_affine(np.zeros((1, 64), np.float32))
+    assert np.all(q == 0) and b[0, 0] == 0 and abs(s[0, 0]) == np.float32(1e-7)
+
+
+def test_quantize_affine_properties():
+    rng = np.random.default_rng(0)
+    w = rng.standard_normal((64, 640)).astype(np.float32) * rng.uniform(0.01, 3, (64, 1)).astype(np.float32)
+    w[:8] = np.abs(w[:8])          # all-positive groups
+    w[8:16] = -np.abs(w[8:16])     # all-negative groups
+    w[16, 5] = 40.0                # an outlier
+    q, s, b = q8.quantize_affine(w)
+    g = w.reshape(64, 10, 64).astype(np.float64)
+    qg = q.reshape(64, 10, 64).astype(np.float64)
+    s64, b64 = s.astype(np.float64)[..., None], b.astype(np.float64)[..., None]
+    # every value within half a step of its reconstruction (fp32 parameters), except that the
+    # rescale to put 0 on the grid (step edge / q0, |q0| = |bias / step|) can push the far
+    # extreme up to 255 (0.5 / |q0|) steps past code 255, where it is clipped
+    err = np.abs(s64 * qg + b64 - g)
+    q0 = np.maximum(np.abs(b64 / s64), 1.0)
+    assert np.all(err <= np.abs(s64) * (0.5 + 127.5 / q0 + 1e-4))
+    inner = (qg > 0) & (qg < 255)
+    assert np.all(np.where(inner, err, 0) <= np.abs(s64) * (0.5 + 1e-4))
+    # the edge (larger-magnitude extreme) has code 0; the other extreme a code near 255
+    lo, hi = g.min(-1), g.max(-1)
+    edge_is_min = np.abs(lo) > np.abs(hi)
+    edge_idx = np.where(edge_is_min, g.argmin(-1), g.argmax(-1))
+    far_idx = np.where(edge_is_min, g.argmax(-1), g.argmin(-1))
+    assert np.all(np.take_along_axis(qg, edge_idx[..., None], -1) == 0)
+    assert np.all(np.take_along_axis(qg, far_idx[..., None], -1) >= 253)
+    # zero is on the grid: -b / s is an integer (to fp32 precision)
+    z = -b.astype(np.float64) / s.astype(np.float64)
+    assert np.all(np.abs(z - np.rint(z)) <= 1e-3)
+    # the scale's magnitude is the range over 255 up to the rescale by round(edge / scale)
+    rng_s = (hi - lo) / 255
+    assert np.all(np.abs(np.abs(s) - rng_s) <= rng_s * 0.5 / np.maximum(np.abs(np.rint(np.where(edge_is_min, lo, hi) / rng_s)), 1) + 1e-9)
+    # fp16 casts of the parameters (the stored layer) stay within their own rounding
+    q16, s16, b16 = q8.quantize_f16(w)
+    assert np.array_equal(q16, q) and np.array_equal(s16, s.astype(np.float16))

@@ -79,3 +79,44 @@ def test_stack_store_and_recycles():
     ref = tr.stack_forward(z.half().double(), None, blocks, 1)
     assert float((z16 - ref).abs().max()) <= 0.05 * float(ref.abs().max())
     assert not torch.equal(z16, ref)
+
+
+def _blocks64(blocks):
+    return [tr.BlockWeights(b.tri_out.to(D), b.tri_in.to(D),
+                            tr.TransitionWeights(b.trans.ln_w.double(), b.trans.ln_b.double(), b.trans.w1.double(),
+                                                 b.trans.w3.double()))
+            for b in blocks]
+
+
+def test_fp16_reference_scheme_matches_exact_arithmetic_for_one_block():
+    # the emulation of the reference's fp16 trunk (every op output stored in fp16, s_a / 256,
+    # norm_mix eps / 256^2) computes the same function: one block sits within fp16 noise of
+    # fp64 (a dropped rescale, a wrong eps or a swapped operand is off by O(1))
+    g = torch.Generator().manual_seed(5)
+    blocks = tr.draw_blocks(g, 1, 128, 128, 512)
+    z = torch.randn(1, 24, 24, 128, generator=g).half()
+    emu = tr.stack_forward_fp16ref(z.float(), None, blocks).double()
+    ref = tr.stack_forward(z.double(), None, _blocks64(blocks))
+    rms = float((ref - z.double()).pow(2).mean().sqrt())
+    assert float((emu - ref).abs().max()) <= 1e-2 * rms
+    assert torch.equal(emu, emu.half().double())  # every stored value is fp16
+    assert not torch.equal(emu, ref)
+
+
+def test_fp16_reference_scheme_error_floor_of_deep_stacks():
+    # the block-stack workload's depth (8 blocks x 3 recycles): the reference's own fp16 scheme,
+    # and even exact arithmetic with only the residual stream stored in fp16, sit above
+    # 1e-2 x RMS(update) from fp64 in the max norm while staying near 2e-3 normwise, so a
+    # max-norm bar of 1e-2 is out of reach for any fp16 trunk at this depth. Measured at the
+    # workload's L=238: 1.66e-2 (fp16 stream) and 1.75e-2 (reference scheme); here at L=48.
+    g = torch.Generator().manual_seed(0)
+    blocks = tr.draw_blocks(g, 8, 128, 128, 512)
+    z = torch.randn(1, 48, 48, 128, generator=g).half()
+    ref = tr.stack_forward(z.double(), None, _blocks64(blocks), 3)
+    rms = float((ref - z.double()).pow(2).mean().sqrt())
+    emu = tr.stack_forward_fp16ref(z.float(), None, blocks, 3).double()
+    s16 = tr.stack_forward(z.double(), None, _blocks64(blocks), 3, store=torch.float16)
+    for got in (emu, s16):
+        d = got - ref
+        assert 1e-2 * rms < float(d.abs().max()) < 3e-2 * rms
+        assert float(d.pow(2).mean().sqrt()) < 3e-3 * rms
