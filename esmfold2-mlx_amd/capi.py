@@ -30,6 +30,8 @@ SIGNATURES = {
     "tmu_forward": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _int, _int, _int,
                            _int, _int, _int, _int, _vp]),
     "pair_transition": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
+    "pair_transition_ws": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
+    "pair_transition_workspace_bytes": (_sz, [_int, _int, _int, _int, _int]),
     "esmc_layer_norm": (_int, [_vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int, _int, _vp]),
     "esmc_layer_norm_parts": (_int, [_vp, _vp, _int, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int, _int, _vp]),
     "esmc_qk_rope": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _f32, _vp]),

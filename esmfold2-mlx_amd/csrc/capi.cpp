@@ -108,7 +108,7 @@ size_t tmu_workspace_bytes(int B, int L, int c) {
   if (B <= 0 || L <= 0 || c <= 0) return 0;
   const size_t plane = (size_t)B * c * L * tmu_leading_dim(L) * sizeof(esm_half);
   const size_t a256 = (plane + 255) / 256 * 256;
-  return 3 * a256;
+  return (c == 128 ? 3 : 4) * a256;  // a, b, x (and the wide path's LN_in(z) plane)
 }
 
 int tmu_project(const esm_half* z, const esm_half* mask, const float* ln_w, const float* ln_b, float ln_eps,
@@ -182,13 +182,98 @@ int tmu_epilogue(const esm_half* x, int ldx, const esm_half* z, const esm_half* 
   return hip_status(esm::launch_epilogue(e, grid, (hipStream_t)stream), "tmu_epilogue launch");
 }
 
+// The wide path of tmu_forward (C = c, a multiple of 128 other than 128, up to 512): five
+// launches in the workspace planes a | b | x | n (x / 256 as in the narrow path):
+//   n = LN_in(z) (cell-major)  ->  a, b = gate(n W^T) (channel-major, GATE_CM)  ->  x = a b^T
+//   ->  y = LN_mix(x) (cell-major, into plane a)  ->  out = [z +] (y W_e^T) * sigmoid(n W_g^T)
+static int tmu_forward_wide(const esm_half* z, const esm_half* mask, const float* ln_in_w, const float* ln_in_b,
+                            float ln_in_eps, const esm_half* w_bundle, const float* ln_mix_w, const float* ln_mix_b,
+                            float ln_mix_eps, const esm_half* w_emit, const esm_half* w_gate, esm_half* out,
+                            void* workspace, int B, int L, int C, int outgoing, int residual, int out_mask,
+                            void* stream) {
+  const int c = C;
+  hipStream_t st = (hipStream_t)stream;
+  const int ld = tmu_leading_dim(L);
+  const size_t ncell = (size_t)B * L * L;
+  if (ncell * C * 2 >= (1ull << 31)) return fail(ESM_ERR_SHAPE, "tmu_forward: B*L*L*C=%zu exceeds 2^30", ncell * C);
+  const size_t plane = (size_t)B * c * L * ld;
+  const size_t a256 = (plane * sizeof(esm_half) + 255) / 256 * 256 / sizeof(esm_half);
+  half_t* wa = static_cast<half_t*>(workspace);
+  half_t* wb = wa + a256;
+  half_t* wx = wb + a256;
+  half_t* wn = wx + a256;
+  const float kScale = 1.0f / 256.0f;
+  hipError_t e = esm::launch_ln_rows(z, nullptr, false, ln_in_w, ln_in_b, ln_in_eps, wn, ncell, C, st);
+  if (e != hipSuccess) return hip_status(e, "tmu_forward ln_rows launch");
+  esm::WideArgs g{};
+  g.a1 = wn;
+  g.w1 = H(w_bundle);                       // signal rows [s_a | s_b]
+  g.w2 = H(w_bundle) + (size_t)2 * c * C;   // gate rows [g_a | g_b]
+  g.K = C;
+  g.N = 2 * c;
+  g.B = B;
+  g.L = L;
+  g.tiles_per_line = (L + 127) / 128;
+  g.transpose = outgoing ? 0 : 1;
+  g.mask = mask ? H(mask) : nullptr;
+  g.plane_a = wa;
+  g.plane_b = wb;
+  g.c = c;
+  g.ld = ld;
+  if (esm::wide_gemm_blocks(g) > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_forward: too many tiles");
+  e = esm::launch_wide_gemm(g, esm::kWideGateCM, st);
+  if (e != hipSuccess) return hip_status(e, "tmu_forward gate launch");
+  esm::ContractArgs ca{wa, wb, wx, B * c, L, ld, ld, kScale};
+  e = esm::launch_contract(ca, st);
+  if (e != hipSuccess) return hip_status(e, "tmu_forward contract launch");
+  e = esm::launch_ln_cf_to_cl(wx, ld, ln_mix_w, ln_mix_b, ln_mix_eps * kScale * kScale, wa, B, L, c, st);
+  if (e != hipSuccess) return hip_status(e, "tmu_forward ln_cf_to_cl launch");
+  esm::WideArgs r{};
+  r.a1 = wa;                                // y = LN_mix(x), cell-major
+  r.w1 = H(w_emit);
+  r.a2 = wn;                                // n = LN_in(z)
+  r.w2 = H(w_gate);
+  r.K = C;
+  r.N = C;
+  r.B = B;
+  r.L = L;
+  r.tiles_per_line = (L + 127) / 128;
+  r.out = H(out);
+  r.ldo = C;
+  r.z = H(z);
+  r.residual = residual ? 1 : 0;
+  r.mask = mask ? H(mask) : nullptr;
+  r.out_mask = out_mask ? 1 : 0;
+  e = esm::launch_wide_gemm(r, esm::kWideResGate, st);
+  return hip_status(e, "tmu_forward emit launch");
+}
+
+static bool wide_width(int C) { return C != 128 && C % 128 == 0 && C <= 512; }
+
 int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, const float* ln_in_b, float ln_in_eps,
                 const esm_half* w_bundle, const float* ln_mix_w, const float* ln_mix_b, float ln_mix_eps,
                 const esm_half* w_emit, const esm_half* w_gate, esm_half* out, void* workspace, int B, int L, int C,
                 int c, int outgoing, int residual, int out_mask, void* stream) {
   if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_forward: B=%d L=%d must be >= 0", B, L);
-  if (C != 128 || c != 128) return fail(ESM_ERR_UNSUPPORTED, "tmu_forward: C=%d c=%d (supported: 128, 128)", C, c);
+  if (!((C == 128 && c == 128) || (C == c && wide_width(C))))
+    return fail(ESM_ERR_UNSUPPORTED, "tmu_forward: C=%d c=%d (supported: C = c, 128 or a multiple of 128 up to 512)",
+                C, c);
   if (B == 0 || L == 0) return ok();
+  if (C != 128) {
+    if (!z || !ln_in_w || !ln_in_b || !w_bundle || !ln_mix_w || !ln_mix_b || !w_emit || !w_gate || !out)
+      return fail(ESM_ERR_NULL, "tmu_forward: NULL pointer");
+    if (!workspace) return fail(ESM_ERR_NULL, "tmu_forward: NULL workspace");
+    if (L > kMaxL) return fail(ESM_ERR_SHAPE, "tmu_forward: L=%d exceeds %d", L, kMaxL);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(ESM_ERR_ALIGN, "tmu_forward: workspace must be 256-byte aligned");
+    if (!aligned16(z) || !aligned16(w_bundle) || !aligned16(w_emit) || !aligned16(w_gate) || !aligned16(out))
+      return fail(ESM_ERR_ALIGN, "tmu_forward: z, weights and out must be 16-byte aligned");
+    if (out == z && !residual) return fail(ESM_ERR_SHAPE, "tmu_forward: out may alias z only with residual=1");
+    if (out_mask && !mask) return fail(ESM_ERR_NULL, "tmu_forward: out_mask=1 needs a mask");
+    if (!(ln_in_eps >= 0.f) || !(ln_mix_eps >= 0.f)) return fail(ESM_ERR_SHAPE, "tmu_forward: eps must be >= 0");
+    return tmu_forward_wide(z, mask, ln_in_w, ln_in_b, ln_in_eps, w_bundle, ln_mix_w, ln_mix_b, ln_mix_eps, w_emit,
+                            w_gate, out, workspace, B, L, C, outgoing, residual, out_mask, stream);
+  }
   if (!workspace) return fail(ESM_ERR_NULL, "tmu_forward: NULL workspace");
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
     return fail(ESM_ERR_ALIGN, "tmu_forward: workspace must be 256-byte aligned");
@@ -283,26 +368,89 @@ int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_
   return q8_linear_ws(x, q, s, b, nullptr, y, M, K, N, group, nullptr, 0, stream);
 }
 
-int pair_transition(const esm_half* z, esm_half* out, const float* ln_w, const float* ln_b, float eps,
-                    const esm_half* w1, const esm_half* w2, const esm_half* w3, int B, int L, int C, int hidden,
-                    void* stream) {
+// The register-resident transition kernel covers C = 128 with ReLU at H in {256, 512} and
+// SwiGLU at H = 256; every other shape runs the wide path (LayerNorm, then one GEMM with the
+// activation fused, then one with the residual fused), whose hidden activations [cells, H]
+// and LayerNormed input [cells, C] live in the caller's workspace.
+static bool narrow_transition(int C, int H, bool swiglu) {
+  return C == 128 && (swiglu ? H == 256 : (H == 256 || H == 512));
+}
+
+size_t pair_transition_workspace_bytes(int B, int L, int C, int hidden, int swiglu) {
+  if (B <= 0 || L <= 0 || C <= 0 || hidden <= 0 || narrow_transition(C, hidden, swiglu != 0)) return 0;
+  const size_t cells = (size_t)B * L * L;
+  const auto al = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
+  return al(cells * C * sizeof(esm_half)) + al(cells * hidden * sizeof(esm_half));
+}
+
+int pair_transition_ws(const esm_half* z, esm_half* out, const float* ln_w, const float* ln_b, float eps,
+                       const esm_half* w1, const esm_half* w2, const esm_half* w3, int B, int L, int C, int hidden,
+                       void* workspace, size_t workspace_bytes, void* stream) {
   if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "pair_transition: B=%d L=%d must be >= 0", B, L);
-  if (C != 128) return fail(ESM_ERR_UNSUPPORTED, "pair_transition: C=%d (supported: 128)", C);
-  if (w2 ? hidden != 256 : (hidden != 256 && hidden != 512))
-    return fail(ESM_ERR_UNSUPPORTED, "pair_transition: H=%d (supported: ReLU 256 or 512, SwiGLU 256)", hidden);
+  const bool narrow = narrow_transition(C, hidden, w2 != nullptr);
+  if (!narrow && !((C == 128 || wide_width(C)) && hidden > 0 && hidden % 32 == 0))
+    return fail(ESM_ERR_UNSUPPORTED,
+                "pair_transition: C=%d H=%d (supported: C a multiple of 128 up to 512, H a multiple of 32)", C, hidden);
   if (!(eps >= 0.f)) return fail(ESM_ERR_SHAPE, "pair_transition: eps must be >= 0");
   if (B == 0 || L == 0) return ok();
   if (L > kMaxL) return fail(ESM_ERR_SHAPE, "pair_transition: L=%d exceeds %d", L, kMaxL);
   const size_t ncells = (size_t)B * L * L;
-  if (ncells * C * 2 >= (1ull << 31)) return fail(ESM_ERR_SHAPE, "pair_transition: B*L*L=%zu cells exceed 2 GB", ncells);
+  if (ncells * (C > hidden ? C : hidden) * 2 >= (1ull << 31))
+    return fail(ESM_ERR_SHAPE, "pair_transition: B*L*L=%zu cells exceed 2 GB of activations", ncells);
   if (!z || !out || !ln_w || !ln_b || !w1 || !w3) return fail(ESM_ERR_NULL, "pair_transition: NULL pointer");
   if (!aligned16(z) || !aligned16(out) || !aligned16(w1) || !aligned16(w3) || (w2 && !aligned16(w2)))
     return fail(ESM_ERR_ALIGN, "pair_transition: z, out, w1, w2, w3 must be 16-byte aligned");
-  esm::TransitionArgs a{H(z), H(out), ln_w, ln_b, eps, H(w1), w2 ? H(w2) : nullptr, H(w3), ncells, 0, hidden};
-  const size_t ntiles = (ncells + 31) / 32;
-  a.ntiles = (int)ntiles;
-  const int grid = (int)(ntiles < (size_t)cu_count() ? ntiles : cu_count());
-  return hip_status(esm::launch_transition(a, grid, (hipStream_t)stream), "pair_transition launch");
+  hipStream_t st = (hipStream_t)stream;
+  if (narrow) {
+    esm::TransitionArgs a{H(z), H(out), ln_w, ln_b, eps, H(w1), w2 ? H(w2) : nullptr, H(w3), ncells, 0, hidden};
+    const size_t ntiles = (ncells + 31) / 32;
+    a.ntiles = (int)ntiles;
+    const int grid = (int)(ntiles < (size_t)cu_count() ? ntiles : cu_count());
+    return hip_status(esm::launch_transition(a, grid, st), "pair_transition launch");
+  }
+  const size_t need = pair_transition_workspace_bytes(B, L, C, hidden, w2 != nullptr);
+  if (!workspace) return fail(ESM_ERR_NULL, "pair_transition: C=%d H=%d needs a workspace of %zu bytes", C, hidden, need);
+  if (workspace_bytes < need)
+    return fail(ESM_ERR_SHAPE, "pair_transition: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(ESM_ERR_ALIGN, "pair_transition: workspace must be 256-byte aligned");
+  half_t* wn = static_cast<half_t*>(workspace);
+  half_t* wh = wn + (ncells * C * sizeof(esm_half) + 255) / 256 * 256 / sizeof(esm_half);
+  hipError_t e = esm::launch_ln_rows(z, nullptr, false, ln_w, ln_b, eps, wn, ncells, C, st);
+  if (e != hipSuccess) return hip_status(e, "pair_transition ln_rows launch");
+  esm::WideArgs g{};
+  g.a1 = wn;
+  g.w1 = H(w1);
+  g.w2 = w2 ? H(w2) : nullptr;
+  g.K = C;
+  g.N = hidden;
+  g.B = B;
+  g.L = L;
+  g.tiles_per_line = (L + 127) / 128;
+  g.out = wh;
+  g.ldo = hidden;
+  if (esm::wide_gemm_blocks(g) > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "pair_transition: too many tiles");
+  e = esm::launch_wide_gemm(g, w2 ? esm::kWideSwiglu : esm::kWideRelu, st);
+  if (e != hipSuccess) return hip_status(e, "pair_transition hidden launch");
+  esm::WideArgs r{};
+  r.a1 = wh;
+  r.w1 = H(w3);
+  r.K = hidden;
+  r.N = C;
+  r.B = B;
+  r.L = L;
+  r.tiles_per_line = (L + 127) / 128;
+  r.out = H(out);
+  r.ldo = C;
+  r.z = H(z);
+  e = esm::launch_wide_gemm(r, esm::kWideResid, st);
+  return hip_status(e, "pair_transition output launch");
+}
+
+int pair_transition(const esm_half* z, esm_half* out, const float* ln_w, const float* ln_b, float eps,
+                    const esm_half* w1, const esm_half* w2, const esm_half* w3, int B, int L, int C, int hidden,
+                    void* stream) {
+  return pair_transition_ws(z, out, ln_w, ln_b, eps, w1, w2, w3, B, L, C, hidden, nullptr, 0, stream);
 }
 
 // esmc_layer_norm and esmc_layer_norm_parts: y (fp16) or yp (fp32 partials of y), or neither.
@@ -377,7 +525,7 @@ int esmc_swiglu(const esm_half* x12, esm_half* y, int M, int F, void* stream) {
 int parcae_step(const float* z, const float* z_init, const float* refined, const float* ln_w, const float* ln_b,
                 float eps, const float* a, const esm_half* b_mat, float* z_out, int B, int L, int C, void* stream) {
   if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "parcae_step: B=%d L=%d must be >= 0", B, L);
-  if (C != 128) return fail(ESM_ERR_UNSUPPORTED, "parcae_step: C=%d (supported: 128)", C);
+  if (C != 128 && C != 256) return fail(ESM_ERR_UNSUPPORTED, "parcae_step: C=%d (supported: 128, 256)", C);
   if (!(eps >= 0.f)) return fail(ESM_ERR_SHAPE, "parcae_step: eps must be >= 0");
   if (B == 0 || L == 0) return ok();
   const size_t ncells = (size_t)B * L * L;
@@ -387,7 +535,7 @@ int parcae_step(const float* z, const float* z_init, const float* refined, const
   if (!aligned16(z) || !aligned16(z_init) || !aligned16(refined) || !aligned16(z_out) || !aligned16(b_mat))
     return fail(ESM_ERR_ALIGN, "parcae_step: z, z_init, refined, z_out, b_mat must be 16-byte aligned");
   const size_t ntiles = (ncells + 31) / 32;
-  esm::ParcaeArgs args{z, z_init, refined, ln_w, ln_b, eps, a, H(b_mat), z_out, ncells, (int)ntiles};
+  esm::ParcaeArgs args{z, z_init, refined, ln_w, ln_b, eps, a, H(b_mat), z_out, ncells, (int)ntiles, C};
   const int grid = (int)(ntiles < (size_t)cu_count() ? ntiles : cu_count());
   return hip_status(esm::launch_parcae_step(args, grid, (hipStream_t)stream), "parcae_step launch");
 }
@@ -395,13 +543,14 @@ int parcae_step(const float* z, const float* z_init, const float* refined, const
 int distogram_expected_distance(const float* r, const esm_half* w, const float* bias, const float* centers, float* ed,
                                 int B, int L, int C, int nbins, void* stream) {
   if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "distogram_expected_distance: B=%d L=%d", B, L);
-  if (C != 128 || (nbins != 64 && nbins != 128))
-    return fail(ESM_ERR_UNSUPPORTED, "distogram_expected_distance: C=%d nbins=%d (C 128; 64 or 128 bins)", C, nbins);
+  if ((C != 128 && C != 256) || (nbins != 64 && nbins != 128))
+    return fail(ESM_ERR_UNSUPPORTED, "distogram_expected_distance: C=%d nbins=%d (C 128 or 256; 64 or 128 bins)", C,
+                nbins);
   if (B == 0 || L == 0) return ok();
   if (L > kMaxL) return fail(ESM_ERR_SHAPE, "distogram_expected_distance: L=%d exceeds %d", L, kMaxL);
   if (!r || !w || !bias || !centers || !ed) return fail(ESM_ERR_NULL, "distogram_expected_distance: NULL pointer");
   if (!aligned16(r) || !aligned16(w)) return fail(ESM_ERR_ALIGN, "distogram_expected_distance: r, w must be 16-byte aligned");
-  esm::DistoArgs args{r, H(w), bias, centers, ed, B, L, nbins};
+  esm::DistoArgs args{r, H(w), bias, centers, ed, B, L, nbins, C};
   const long long tiles = (long long)B * L * ((L + 127) / 128);
   const int grid = (int)(tiles < 4LL * cu_count() ? tiles : 4LL * cu_count());
   return hip_status(esm::launch_expected_distance(args, grid, (hipStream_t)stream), "distogram_expected_distance launch");

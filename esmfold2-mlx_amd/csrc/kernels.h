@@ -130,6 +130,7 @@ struct ParcaeArgs {
   float* z_out;           // [cells, C], may be z
   size_t ncells;
   int ntiles;
+  int C;                  // 128 or 256
 };
 
 struct DistoArgs {
@@ -139,6 +140,30 @@ struct DistoArgs {
   const float* centers;   // [nbins]
   float* ed;              // [B, L, L]
   int B, L, nbins;
+  int C;                  // 128 or 256
+};
+
+// Wide path (pair widths other than 128): epilogues of wide_gemm.
+enum : int { kWideGateCM = 0, kWideResGate = 1, kWideRelu = 2, kWideSwiglu = 3, kWideResid = 4 };
+
+struct WideArgs {
+  const half_t* a1;     // [cells, K] fp16 rows (the A operand of GEMM 1)
+  const half_t* a2;     // [cells, K] (GEMM 2's A; nullptr or a1: the same operand)
+  const half_t* w1;     // [N, K]
+  const half_t* w2;     // [N, K] or nullptr (single GEMM)
+  int K, N;
+  int B, L;             // cells = B * L * L, tiled along lines of L cells
+  int tiles_per_line;   // ceil(L / 128)
+  int transpose;        // 1: line = column, positions along rows (the incoming operands)
+  half_t* out;          // [cells, ldo] cell-major output (all but GATE_CM)
+  int ldo;
+  const half_t* z;      // [cells, ldo] residual (RESGATE with residual, RESID)
+  int residual;         // RESGATE: add z
+  const half_t* mask;   // [cells] or nullptr (GATE_CM; RESGATE with out_mask)
+  int out_mask;
+  half_t* plane_a;      // GATE_CM: outputs [0, c) -> a, [c, 2c) -> b, [B, c, L, ld] channel-major
+  half_t* plane_b;
+  int c, ld;
 };
 
 // Cells per tile of the per-cell kernels (a) and (c).
@@ -162,6 +187,12 @@ hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s);
 hipError_t launch_esmc_attention(const EsmcAttnArgs& a, hipStream_t s);
 hipError_t launch_esmc_swiglu(const half_t* x12, half_t* y, size_t M, int F, hipStream_t s);
 hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st);
+hipError_t launch_ln_rows(const void* x, const float* x2, bool in_f32, const float* w, const float* b, float eps,
+                          half_t* out, size_t rows, int C, hipStream_t s);
+hipError_t launch_ln_cf_to_cl(const half_t* x, int ldx, const float* w, const float* b, float eps, half_t* y, int B,
+                              int L, int c, hipStream_t s);
+long long wide_gemm_blocks(const WideArgs& a);
+hipError_t launch_wide_gemm(const WideArgs& a, int epi, hipStream_t s);
 hipError_t launch_q8_quantize(const float* w, uint8_t* q, half_t* s, half_t* b, int N, int K, hipStream_t st);
 hipError_t launch_q8_dequant(const uint8_t* q, const half_t* s, const half_t* b, half_t* w, int N, int K,
                              hipStream_t st);

@@ -3,44 +3,49 @@
 //   parcae_step          z <- a * z + LN(z_init + refined) @ B^T on every cell (fp32 state)
 //   expected_distance    softmax((r + r^T) @ W^T + b) . centres per pair (distogram head)
 //   abs_diff_quantile    the q-th quantile (linear interpolation) of |x - y| (exit signal)
-// C = 128 pair channels.
+// C = 128 or 256 pair channels (a template parameter of the first two).
 #include "common.h"
 #include "kernels.h"
 
 namespace esm {
 
-namespace {
-constexpr int C = 128;
-constexpr int NSTR = C + 8;  // LDS row stride (halfs) of a LayerNormed tile
-}  // namespace
-
 // ---- parcae step ----------------------------------------------------------------------------
 // Persistent, 4 waves per workgroup; a tile is 32 consecutive cells. Wave w owns output
-// channels [32w, 32w+32) and keeps those rows of B (fp16) as MFMA A fragments. Per tile:
-// u = z_init + refined, LayerNorm (16 lanes per cell, fp32 statistics) into LDS as fp16,
-// one barrier, D[co][cell] = B[co][:] . LN(u)[cell][:] (fp32 accumulation), then
-// a[co] * z + D in fp32, 16-byte stores (4 consecutive channels per lane and quad).
+// channels [w CC/4, (w+1) CC/4) (OB = CC/128 blocks of 32) and keeps those rows of B (fp16) as
+// MFMA A fragments. Per tile: u = z_init + refined, LayerNorm (16 lanes per cell, lane l
+// holding the 8-channel chunks l + 16 t, fp32 statistics) into LDS as fp16, one barrier,
+// D[co][cell] = B[co][:] . LN(u)[cell][:] (fp32 accumulation), then a[co] * z + D in fp32,
+// 16-byte stores (4 consecutive channels per lane and quad).
+template <int CC>
 __global__ __launch_bounds__(256, 1) void parcae_step_kernel(ParcaeArgs p) {
+  constexpr int OB = CC / 128;       // 32-channel output blocks per wave
+  constexpr int NCH = CC / 128;      // 8-channel chunks per lane in the LayerNorm
+  constexpr int NSTR = CC + 8;       // LDS row stride (halfs) of the LayerNormed tile
   __shared__ __align__(16) half_t n_s[32 * NSTR];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
-  half8 bw[C / 16];
-  {
-    const half_t* row = p.b_mat + (size_t)(32 * wave + r) * C;
+  half8 bw[OB][CC / 16];
 #pragma unroll
-    for (int ks = 0; ks < C / 16; ks++) bw[ks] = ld16(row + 16 * ks + 8 * h);
+  for (int ob = 0; ob < OB; ob++) {
+    const half_t* row = p.b_mat + (size_t)(wave * (CC / 4) + 32 * ob + r) * CC;
+#pragma unroll
+    for (int ks = 0; ks < CC / 16; ks++) bw[ob][ks] = ld16(row + 16 * ks + 8 * h);
   }
-  const int ch0 = (lane & 15) * 8;
-  float g[8], bb[8];
+  const int l16 = lane & 15;
+  float g[NCH][8], bb[NCH][8];
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    g[e] = p.ln_w[ch0 + e];
-    bb[e] = p.ln_b[ch0 + e];
-  }
-  float av[16];  // a for this lane's 16 output channels
+  for (int t = 0; t < NCH; t++)
 #pragma unroll
-  for (int i = 0; i < 16; i++) av[i] = p.a[32 * wave + acc_row32(i, lane)];
+    for (int e = 0; e < 8; e++) {
+      g[t][e] = p.ln_w[8 * (l16 + 16 * t) + e];
+      bb[t][e] = p.ln_b[8 * (l16 + 16 * t) + e];
+    }
+  float av[OB][16];  // a for this lane's output channels
+#pragma unroll
+  for (int ob = 0; ob < OB; ob++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) av[ob][i] = p.a[wave * (CC / 4) + 32 * ob + acc_row32(i, lane)];
 
   const rsrc_t rz = make_rsrc(p.z), ri = make_rsrc(p.z_init), rr = make_rsrc(p.refined), ro = make_rsrc(p.z_out);
   const size_t ncells = p.ncells;
@@ -50,40 +55,69 @@ __global__ __launch_bounds__(256, 1) void parcae_step_kernel(ParcaeArgs p) {
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int cl = (tid >> 4) + 16 * i;
-      const uint32_t off = cell0 + cl < ncells ? (uint32_t)(((cell0 + cl) * C + ch0) * 4u) : kOOB;
-      float v[8];
+      const bool live = cell0 + cl < ncells;
+      float v[NCH][8];
 #pragma unroll
-      for (int hh = 0; hh < 2; hh++) {
-        const f32x4 a4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ri, (int)(off + 16u * hh), 0, 0));
-        const f32x4 b4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, (int)(off + 16u * hh), 0, 0));
+      for (int t = 0; t < NCH; t++) {
+        const uint32_t off = live ? (uint32_t)(((cell0 + cl) * CC + 8 * (l16 + 16 * t)) * 4u) : kOOB;
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[4 * hh + e] = a4[e] + b4[e];
+        for (int hh = 0; hh < 2; hh++) {
+          const f32x4 a4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ri, (int)(off + 16u * hh), 0, 0));
+          const f32x4 b4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, (int)(off + 16u * hh), 0, 0));
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[t][4 * hh + e] = a4[e] + b4[e];
+        }
       }
-      ln_row128(v, g, bb, p.eps);
-      half8 o;
+      float s = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) o[e] = (half_t)v[e];
-      st16(&n_s[cl * NSTR + ch0], o);
+      for (int t = 0; t < NCH; t++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) s += v[t][e];
+      const float mean = row16_sum(s) * (1.0f / CC);
+      float q = 0.f;
+#pragma unroll
+      for (int t = 0; t < NCH; t++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          v[t][e] -= mean;
+          q += v[t][e] * v[t][e];
+        }
+      const float rstd = rsqrtf(row16_sum(q) * (1.0f / CC) + p.eps);
+#pragma unroll
+      for (int t = 0; t < NCH; t++) {
+        half8 o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = (half_t)(v[t][e] * rstd * g[t][e] + bb[t][e]);
+        st16(&n_s[cl * NSTR + 8 * (l16 + 16 * t)], o);
+      }
     }
     __syncthreads();
-    // 2. D[co][cell] over the wave's 32 output channels
-    f32x16 d;
+    // 2. D[co][cell] over the wave's output channels
+    f32x16 d[OB];
 #pragma unroll
-    for (int i = 0; i < 16; i++) d[i] = 0.f;
+    for (int ob = 0; ob < OB; ob++)
 #pragma unroll
-    for (int ks = 0; ks < C / 16; ks++) d = mfma32(bw[ks], ld16(&n_s[r * NSTR + 16 * ks + 8 * h]), d);
-    // 3. a * z + D for the lane's cell and 4 quads of 4 consecutive channels
+      for (int i = 0; i < 16; i++) d[ob][i] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < CC / 16; ks++) {
+      const half8 nb = ld16(&n_s[r * NSTR + 16 * ks + 8 * h]);
+#pragma unroll
+      for (int ob = 0; ob < OB; ob++) d[ob] = mfma32(bw[ob][ks], nb, d[ob]);
+    }
+    // 3. a * z + D for the lane's cell and 4 quads of 4 consecutive channels per block
     const bool live = cell0 + r < ncells;
 #pragma unroll
-    for (int r4 = 0; r4 < 4; r4++) {
-      const int co = 32 * wave + acc_row32(4 * r4, lane);
-      const uint32_t off = live ? (uint32_t)(((cell0 + r) * C + co) * 4u) : kOOB;
-      const f32x4 z4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rz, (int)off, 0, 0));
-      f32x4 o;
+    for (int ob = 0; ob < OB; ob++)
 #pragma unroll
-      for (int e = 0; e < 4; e++) o[e] = av[4 * r4 + e] * z4[e] + d[4 * r4 + e];
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, (int)off, 0, 0);
-    }
+      for (int r4 = 0; r4 < 4; r4++) {
+        const int co = wave * (CC / 4) + 32 * ob + acc_row32(4 * r4, lane);
+        const uint32_t off = live ? (uint32_t)(((cell0 + r) * CC + co) * 4u) : kOOB;
+        const f32x4 z4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rz, (int)off, 0, 0));
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = av[ob][4 * r4 + e] * z4[e] + d[ob][4 * r4 + e];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, (int)off, 0, 0);
+      }
     __syncthreads();  // n_s is rewritten by the next tile
   }
 }
@@ -91,24 +125,36 @@ __global__ __launch_bounds__(256, 1) void parcae_step_kernel(ParcaeArgs p) {
 // ---- expected distance ----------------------------------------------------------------------
 // One wave per 32 pairs (b, i, j0 .. j0+31); 4 waves per workgroup. The B operand is
 // s[cell][c] = r[b,i,j,c] + r[b,j,i,c] rounded to fp16, read straight into fragments
-// (column = pair, k = channel); A = the head's weight rows (bins). A lane then holds its
-// pair's logits for 16 bins per 32-bin block: the softmax over bins is a register
-// reduction plus one exchange between the lane halves. Bias and centres come from LDS.
-template <int NBB>  // 32-bin blocks
+// (column = pair, k = channel); A = the head's weight rows (bins), held in registers, or
+// for the widest heads (128 bins at 256 channels: 256 registers of fragments) read from an
+// LDS copy per k-step. A lane then holds its pair's logits for 16 bins per 32-bin block: the
+// softmax over bins is a register reduction plus one exchange between the lane halves.
+// Bias and centres come from LDS.
+template <int NBB, int CC>  // 32-bin blocks, channels
 __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) {
   constexpr int NB = 32 * NBB;
+  constexpr bool WLDS = NBB * CC > 512;   // fragments from LDS instead of registers
+  constexpr int WS = CC + 8;              // LDS row stride (halfs) of the weight copy
   __shared__ float bias_s[NB], cent_s[NB];
+  __shared__ __align__(16) half_t w_s[WLDS ? NB * WS : 8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, h = lane >> 5;
   for (int k = tid; k < NB; k += 256) {
     bias_s[k] = p.bias[k];
     cent_s[k] = p.centers[k];
   }
-  half8 wa[NBB][C / 16];
+  half8 wa[WLDS ? 1 : NBB][WLDS ? 1 : CC / 16];
+  if constexpr (WLDS) {
+    for (int q = tid; q < NB * (CC / 8); q += 256) {
+      const int row = q / (CC / 8), j = q - row * (CC / 8);
+      st16(&w_s[row * WS + 8 * j], ld16(p.w + (size_t)row * CC + 8 * j));
+    }
+  } else {
 #pragma unroll
-  for (int bb = 0; bb < NBB; bb++)
+    for (int bb = 0; bb < NBB; bb++)
 #pragma unroll
-    for (int ks = 0; ks < C / 16; ks++) wa[bb][ks] = ld16(p.w + (size_t)(32 * bb + r) * C + 16 * ks + 8 * h);
+      for (int ks = 0; ks < CC / 16; ks++) wa[bb][ks] = ld16(p.w + (size_t)(32 * bb + r) * CC + 16 * ks + 8 * h);
+  }
   __syncthreads();
 
   const int L = p.L;
@@ -118,15 +164,15 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
     const int b = bi / L, i = bi - b * L;
     const int j = j0 + r;
     const bool live = j < L;
-    const float* rij = p.r + (((size_t)b * L + i) * L + (live ? j : 0)) * C;
-    const float* rji = p.r + (((size_t)b * L + (live ? j : 0)) * L + i) * C;
+    const float* rij = p.r + (((size_t)b * L + i) * L + (live ? j : 0)) * CC;
+    const float* rji = p.r + (((size_t)b * L + (live ? j : 0)) * L + i) * CC;
     f32x16 d[NBB];
 #pragma unroll
     for (int bb = 0; bb < NBB; bb++)
 #pragma unroll
       for (int e = 0; e < 16; e++) d[bb][e] = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < C / 16; ks++) {
+    for (int ks = 0; ks < CC / 16; ks++) {
       const int c0 = 16 * ks + 8 * h;
       half8 s;
 #pragma unroll
@@ -137,7 +183,10 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
         for (int e = 0; e < 4; e++) s[4 * hh + e] = (half_t)(x[e] + y[e]);
       }
 #pragma unroll
-      for (int bb = 0; bb < NBB; bb++) d[bb] = mfma32(wa[bb][ks], s, d[bb]);
+      for (int bb = 0; bb < NBB; bb++) {
+        const half8 w = WLDS ? ld16(&w_s[(32 * bb + r) * WS + c0]) : wa[WLDS ? 0 : bb][WLDS ? 0 : ks];
+        d[bb] = mfma32(w, s, d[bb]);
+      }
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -317,15 +366,24 @@ __global__ __launch_bounds__(QT) void abs_diff_quantile_kernel(const float* __re
 }
 
 hipError_t launch_parcae_step(const ParcaeArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL(parcae_step_kernel, dim3(grid), dim3(256), 0, s, a);
+  if (a.C == 128)
+    hipLaunchKernelGGL(parcae_step_kernel<128>, dim3(grid), dim3(256), 0, s, a);
+  else if (a.C == 256)
+    hipLaunchKernelGGL(parcae_step_kernel<256>, dim3(grid), dim3(256), 0, s, a);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 hipError_t launch_expected_distance(const DistoArgs& a, int grid, hipStream_t s) {
-  if (a.nbins == 64)
-    hipLaunchKernelGGL(expected_distance_kernel<2>, dim3(grid), dim3(256), 0, s, a);
-  else if (a.nbins == 128)
-    hipLaunchKernelGGL(expected_distance_kernel<4>, dim3(grid), dim3(256), 0, s, a);
+  if (a.nbins == 64 && a.C == 128)
+    hipLaunchKernelGGL((expected_distance_kernel<2, 128>), dim3(grid), dim3(256), 0, s, a);
+  else if (a.nbins == 128 && a.C == 128)
+    hipLaunchKernelGGL((expected_distance_kernel<4, 128>), dim3(grid), dim3(256), 0, s, a);
+  else if (a.nbins == 64 && a.C == 256)
+    hipLaunchKernelGGL((expected_distance_kernel<2, 256>), dim3(grid), dim3(256), 0, s, a);
+  else if (a.nbins == 128 && a.C == 256)
+    hipLaunchKernelGGL((expected_distance_kernel<4, 256>), dim3(grid), dim3(256), 0, s, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

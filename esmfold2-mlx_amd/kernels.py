@@ -11,7 +11,7 @@ import ctypes
 
 import torch
 
-from . import capi
+from . import capi, scratch
 
 F16 = torch.float16
 
@@ -102,7 +102,8 @@ def epilogue(x, z, mask, ln_in_w, ln_in_b, eps_in, ln_mix_w, ln_mix_b, eps_mix, 
 
 def transition(z, ln_w, ln_b, eps, w1, w3, w2=None, out=None):
     """Kernel (e): z + W3 act(W1 LN(z)), act = ReLU (``w2`` None) or silu(W1 h) * (W2 h).
-    z [B, L, L, C] fp16; w1, w2 [H, C], w3 [C, H] fp16; ``out`` may be ``z`` (in place)."""
+    z [B, L, L, C] fp16; w1, w2 [H, C], w3 [C, H] fp16; ``out`` may be ``z`` (in place). Shapes
+    outside the register-resident kernel's run the wide path in the device's shared scratch."""
     lib = capi.lib()
     _dev(z, "z", F16)
     B, L, L2, C = z.shape
@@ -116,9 +117,11 @@ def transition(z, ln_w, ln_b, eps, w1, w3, w2=None, out=None):
     if tuple(w1.shape) != (H, C) or tuple(w3.shape) != (C, H) or (w2 is not None and tuple(w2.shape) != (H, C)):
         raise capi.EsmError(-2, f"transition: w1 {tuple(w1.shape)}, w3 {tuple(w3.shape)} for C={C}")
     out = torch.empty_like(z) if out is None else _out(out, "out", F16, z.numel())
-    capi.check(lib.pair_transition(z.data_ptr(), out.data_ptr(), _dev(ln_w, "ln_w", torch.float32).data_ptr(),
-                                   _dev(ln_b, "ln_b", torch.float32).data_ptr(), float(eps), w1.data_ptr(), _ptr(w2),
-                                   w3.data_ptr(), B, L, C, H, capi.stream_ptr()))
+    need = int(lib.pair_transition_workspace_bytes(B, L, C, H, int(w2 is not None)))
+    ws = scratch.get(need, z.device) if need else None  # the wide path's LN(z) and hidden planes
+    capi.check(lib.pair_transition_ws(z.data_ptr(), out.data_ptr(), _dev(ln_w, "ln_w", torch.float32).data_ptr(),
+                                      _dev(ln_b, "ln_b", torch.float32).data_ptr(), float(eps), w1.data_ptr(),
+                                      _ptr(w2), w3.data_ptr(), B, L, C, H, _ptr(ws), need, capi.stream_ptr()))
     return out
 
 

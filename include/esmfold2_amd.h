@@ -52,7 +52,8 @@ const char* esm_source_hash(void);
 
 /* Bytes of caller-provided workspace tmu_forward needs for B x L x L cells with
  * c latent channels: two operands [B, c, L, ld] and the contraction output
- * [B, c, L, ld], fp16, with ld = tmu_leading_dim(L). */
+ * [B, c, L, ld], fp16, with ld = tmu_leading_dim(L); for c != 128 (the wide path) a
+ * fourth plane holds LN_in(z). Each plane starts 256-byte aligned. */
 size_t tmu_workspace_bytes(int B, int L, int c);
 
 /* Padded row length (elements) of the channel-major operands: L rounded up to 8,
@@ -142,6 +143,11 @@ int tmu_epilogue(const esm_half* x, int ldx, const esm_half* z, const esm_half* 
  *
  * workspace: tmu_workspace_bytes(B, L, c) bytes, 256-byte aligned, caller-owned.
  * outgoing: 1 = "outgoing edges" update, 0 = "incoming edges".
+ * Supported: C = c = 128 (kernels (a), (b), (c)), or C = c a multiple of 128 up to 512
+ * (ESMFold2's trunk is 256 wide, mlx_trunk.py:3-5): the wide path, five launches with
+ * the same arithmetic (LN_in(z) -> gated projection stored channel-major -> kernel (b)
+ * -> LN_mix over channels turned cell-major -> emit and gate GEMMs with the residual).
+ * B * L * L * C < 2^30.
  */
 int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, const float* ln_in_b, float ln_in_eps,
                 const esm_half* w_bundle, const float* ln_mix_w, const float* ln_mix_b, float ln_mix_eps,
@@ -159,11 +165,26 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
  * z, out [B, L, L, C] fp16 cell-major (out may be z); ln_w, ln_b [C] fp32;
  * w1, w2 [H, C] fp16; w3 [C, H] fp16 (torch [out, in] layouts). fp32 statistics and
  * accumulation; the hidden activations and the output are each rounded once to fp16.
- * Supported: C = 128; ReLU H = 256 or 512; SwiGLU H = 256.
+ * Without a workspace: C = 128 with ReLU at H = 256 or 512, or SwiGLU at H = 256 (one
+ * register-resident kernel). Other shapes need pair_transition_ws.
  */
 int pair_transition(const esm_half* z, esm_half* out, const float* ln_w, const float* ln_b, float eps,
                     const esm_half* w1, const esm_half* w2, const esm_half* w3, int B, int L, int C, int H,
                     void* stream);
+
+/*
+ * pair_transition for every supported shape: C a multiple of 128 up to 512 and H a
+ * multiple of 32 (ESMFold2's 256-wide trunk with its SwiGLU hidden width). The shapes
+ * pair_transition covers run its kernel and ignore the workspace; the others run LN(z),
+ * then one GEMM with the activation fused (hidden [cells, H] fp16, rounded once), then one
+ * with the residual fused, in `workspace` of at least
+ * pair_transition_workspace_bytes(B, L, C, H, swiglu) bytes (256-byte aligned; 0 bytes
+ * when none is needed). out may be z.
+ */
+size_t pair_transition_workspace_bytes(int B, int L, int C, int H, int swiglu);
+int pair_transition_ws(const esm_half* z, esm_half* out, const float* ln_w, const float* ln_b, float eps,
+                       const esm_half* w1, const esm_half* w2, const esm_half* w3, int B, int L, int C, int H,
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Kernel (d): MLX-affine 8-bit weight-only linear, y = x . W^T with
@@ -271,12 +292,12 @@ int esmc_swiglu(const esm_half* x12, esm_half* y, int M, int F, void* stream);
  *   cell (var_6b_mlx_loop.py:67-71: u = z_init + lm_encoder(lm_z), the "parcae"
  *   linear recurrence, fp32). z, z_init, refined, z_out [B, L, L, C] fp32 (z_out may be
  *   z); ln_w, ln_b, a [C] fp32; b_mat [C, C] fp16 (torch [out, in]). LayerNorm in fp32,
- *   its output and B rounded to fp16 for the MFMA, fp32 accumulation and update. C = 128.
+ *   its output and B rounded to fp16 for the MFMA, fp32 accumulation and update. C = 128 or 256.
  * distogram_expected_distance: ed = softmax((r + r^T) @ W^T + bias) . centers per pair
  *   (var_6b_mlx_loop.py:74-76; var_adaptive_loops.py:41-46), r^T swapping the two
  *   residue axes. r [B, L, L, C] fp32 (the readout or the coda output); w [nbins, C] fp16
  *   (the head's weight); bias, centers [nbins] fp32; ed [B, L, L] fp32. The pair sums are
- *   rounded to fp16 for the MFMA; logits and softmax in fp32. C = 128, nbins 64 or 128.
+ *   rounded to fp16 for the MFMA; logits and softmax in fp32. C = 128 or 256, nbins 64 or 128.
  * abs_diff_quantile: out[0] = the q-th quantile of |x - y| (y NULL: of |x|) over n values,
  *   linear interpolation between the two nearest order statistics, as torch.quantile
  *   (the exit signal: var_6b_mlx_loop.py:79-85 with q = 0.95, var_adaptive_loops.py:116).

@@ -57,6 +57,13 @@ def test_rejects_unsupported_channels(lib):
     rc = lib.tmu_forward(*([None] * 4), 1e-5, None, None, None, 1e-5, None, None, None, None, 1, 8, 64, 64, 1, 0, 0,
                          None)
     assert rc == -4
+    # the wide path needs C = c (the reference's TMU has c = C)
+    rc = lib.tmu_forward(*([None] * 4), 1e-5, None, None, None, 1e-5, None, None, None, None, 1, 8, 256, 128, 1, 0,
+                         0, None)
+    assert rc == -4
+    rc = lib.tmu_forward(*([None] * 4), 1e-5, None, None, None, 1e-5, None, None, None, None, 1, 8, 256, 256, 1, 0,
+                         0, None)
+    assert rc == -1
 
 
 def test_rejects_null_and_bad_shapes(lib):
@@ -68,9 +75,18 @@ def test_rejects_null_and_bad_shapes(lib):
     assert lib.q8_dequant(None, None, None, None, 64, 64, 64, None) == -1
     assert lib.q8_linear_ws(None, None, None, None, None, None, 5, 1024, 64, 64, None, 0, None) == -1
     assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 1, 8, 128, 512, None) == -1
-    assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 1, 8, 256, 512, None) == -4
-    assert lib.pair_transition(None, None, None, None, 1e-5, None, ctypes.c_void_p(4096), None, 1, 8, 128, 512,
-                               None) == -4  # SwiGLU at H=512
+    # widths the wide path does not cover: C not a multiple of 128 (or above 512), H not of 32
+    assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 1, 8, 192, 512, None) == -4
+    assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 1, 8, 640, 512, None) == -4
+    assert lib.pair_transition(None, None, None, None, 1e-5, None, ctypes.c_void_p(4096), None, 1, 8, 256, 100,
+                               None) == -4
+    # 256 wide, or SwiGLU at H = 512: supported through the wide path (NULL pointers checked)
+    assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 1, 8, 256, 512, None) == -1
+    assert lib.pair_transition_ws(None, None, None, None, 1e-5, None, ctypes.c_void_p(4096), None, 1, 8, 128, 512,
+                                  None, 0, None) == -1
+    assert lib.pair_transition_workspace_bytes(1, 8, 128, 512, 0) == 0       # the register-resident kernel
+    assert lib.pair_transition_workspace_bytes(1, 8, 128, 512, 1) == 2 * 8 * 8 * 128 + 2 * 8 * 8 * 512
+    assert lib.tmu_workspace_bytes(1, 8, 256) == 4 * 256 * 8 * 8 * 2  # a, b, x and LN_in(z)
     assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 0, 8, 128, 512, None) == 0
     # the partials entry points: a NULL split count, a short buffer, a bad split count
     assert lib.q8_linear_partials(None, None, None, None, None, None, 0, None, 4, 128, 64, 64, None) == -1

@@ -110,12 +110,14 @@ def test_trimul_matches_transformers_openfold(L, C, masked):
     assert _hf_check(tmu.trimul, L=L, C=C, masked=masked) == [False, False]
 
 
-def test_trimul_matches_transformers_fp32_c128():
-    # the configs' width, fp32, nonzero LN params: still the same algorithm
-    g = torch.Generator().manual_seed(11)
+@pytest.mark.parametrize("C", [128, 256])
+def test_trimul_matches_transformers_wide(C):
+    # the configs' width and ESMFold2's real 256 (mlx_trunk.py:3-5), nonzero LN params and a
+    # random mask: still the same algorithm
+    g = torch.Generator().manual_seed(11 + C)
     for outgoing in (True, False):
-        p = _rand_weights(g, 128, 128, outgoing)
-        z = torch.randn(1, 12, 12, 128, generator=g, dtype=D)
+        p = _rand_weights(g, C, C, outgoing)
+        z = torch.randn(1, 12, 12, C, generator=g, dtype=D)
         mask = _rand_mask(g, 1, 12)
         with torch.no_grad():
             ref = _hf_module(p, outgoing)(z, mask)
