@@ -24,6 +24,7 @@ Also reported on the same JSON line:
                 SwiGLU kernels) replayed as one HIP graph, every replay checked
                 against the eager output; the eager time, bound by the 13 host
                 launches, beside it;
+  pair_c256     the same TMU pair at ESMFold2's real width, C = c = 256 (the wide path);
   cpu_baseline  the CPU oracle (torch fp32 restatement of the reference's
                 _trimul_forward) on the host cores, a bounded sample of the same
                 workload (rank 0, N=1 only). This leg also verifies the GPU leg:
@@ -90,6 +91,7 @@ def parse():
                     help="time the transition kernel but skip the HIP-graph block-stack figure")
     ap.add_argument("--no-esmc", action="store_true", help="skip the ESMC block figure")
     ap.add_argument("--no-recycle", action="store_true", help="skip the recycling-step figures")
+    ap.add_argument("--no-wide", action="store_true", help="skip the 256-wide pair figure")
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 64 MiB device copy 10 times (counter calibration under rocprofv3)")
@@ -446,6 +448,31 @@ def main():
         rres["parcae_step"].update({"gbs": pb / rres["parcae_step"]["us"] / 1e3,
                                     "hbm_frac": pb / rres["parcae_step"]["us"] / 1e3 / (HBM_PEAK / 1e9)})
         out["recycle"] = rres
+
+    if not args.no_wide:
+        # the same pair at ESMFold2's real pair width, C = c = 256 (the wide path: five launches
+        # per direction), z [1, 238, 238, 256] fp16
+        zw, _, pow_, piw = W.pair_inputs(L, 256, 256, seed=0, dtype=torch.float16)
+        T = pkg.trimul
+        pair_w = T.TriMulPair(T.TriMul.from_weights(pow_, device=dev), T.TriMul.from_weights(piw, device=dev))
+        zw0 = zw.to(dev)
+        zwo = torch.empty_like(zw0)
+        for _ in range(3):
+            pair_w(zw0, out=zwo)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            pair_w(zw0, out=zwo)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        cw = alg_counts(L, 256, 256)
+        fl = 2 * sum(v["flops"] for v in cw.values())
+        out["pair_c256"] = {"us": t * 1e6, "cells_per_s": L * L / t, "tflops": fl / t / 1e12,
+                            "mfma_frac": fl / t / MFMA_F16_PEAK, "launches": 10,
+                            "workload": "TMU pair out+in with residuals, z [1,238,238,256] fp16, c_hidden 256"}
 
     esmc_case = None
     if not args.no_esmc:
