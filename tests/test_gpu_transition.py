@@ -68,8 +68,16 @@ def test_transition_in_place_and_large(gpu_lib, pkg):
     _check(zd.cpu(), z16, p)
 
 
-def test_transition_rejects_unsupported(gpu_lib, pkg):
-    p = _weights(128, 384, False, seed=0)
+def test_transition_other_hidden_widths_and_unsupported(gpu_lib, pkg):
+    # hidden widths outside the register-resident kernel's run the wide path (LN, then a GEMM
+    # with the activation fused, then one with the residual fused)
+    for H, swiglu in ((384, False), (512, True)):
+        p = _weights(128, H, swiglu, seed=H)
+        z16 = torch.randn(1, 29, 29, 128, generator=torch.Generator().manual_seed(H)).half()
+        _check(_run(pkg, z16.to(DEV), p).cpu(), z16, p)
+    # a hidden width that is not a multiple of 32 is refused before any launch
+    p = _weights(128, 100, False, seed=0)
     z16 = torch.zeros(1, 4, 4, 128, dtype=torch.float16, device=DEV)
-    with pytest.raises(pkg.capi.EsmError):
+    with pytest.raises(pkg.capi.EsmError) as e:
         _run(pkg, z16, p)
+    assert e.value.code == -4
