@@ -42,6 +42,7 @@ SIGNATURES = {
     "abs_diff_quantile": (_int, [_vp, _vp, _sz, _f32, _vp, _vp]),
     "q8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "q8_linear_ws": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
+    "q8_linear_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "q8_linear_workspace_bytes": (_sz, [_int, _int, _int]),
     "q8_linear_partials_bytes": (_sz, [_int, _int, _int]),
     "q8_linear_partials": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _int, _int, _int, _int, _vp]),

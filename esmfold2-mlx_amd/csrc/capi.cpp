@@ -340,6 +340,28 @@ int q8_linear_ws(const esm_half* x, const uint8_t* q, const esm_half* s, const e
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear launch");
 }
 
+int q8_linear_noalloc(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, const uint32_t* sb,
+                      esm_half* y, int M, int K, int N, int group, void* stream) {
+  static_assert(esm::kQ8ScratchBytes == ESM_Q8_NOALLOC_SCRATCH_BYTES, "header and library agree on the scratch");
+  bool empty;
+  if (const int rc = q8_check("q8_linear_noalloc", x, q, s, b, y, 8, M, K, N, group, &empty)) return rc;
+  if (empty) return ok();
+  const Q8Plan pl = q8_plan(M, K, N);
+  if ((long long)pl.mtiles * pl.ntiles * pl.splits > 0x7fffffffLL)
+    return fail(ESM_ERR_SHAPE, "q8_linear_noalloc: M=%d N=%d too large", M, N);
+  if (pl.splits > 1 && pl.bytes > esm::kQ8ScratchBytes)
+    return fail(ESM_ERR_SHAPE, "q8_linear_noalloc: M=%d K=%d N=%d needs %zu bytes of split-K scratch, the static "
+                "scratch holds %zu", M, K, N, pl.bytes, esm::kQ8ScratchBytes);
+  if (sb && !aligned16(sb)) return fail(ESM_ERR_ALIGN, "q8_linear_noalloc: packed scales must be 16-byte aligned");
+  float* part = nullptr;
+  if (pl.splits > 1) {
+    const hipError_t e = esm::q8_scratch_address(&part);
+    if (e != hipSuccess) return hip_status(e, "q8_linear_noalloc: scratch address");
+  }
+  esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits, part, sb};
+  return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_noalloc launch");
+}
+
 size_t q8_linear_partials_bytes(int M, int K, int N) {
   if (M <= 0 || K <= 0 || N <= 0 || K % 64 != 0 || N % 64 != 0 || K > kQ8MaxK) return 0;
   return q8_plan(M, K, N).bytes;

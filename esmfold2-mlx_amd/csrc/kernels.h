@@ -67,6 +67,10 @@ struct Q8Args {
 constexpr int kQ8TileM = 64;
 constexpr int kQ8TileN = 160;
 constexpr int kQ8Waves = 4;
+// Bytes of the device scratch q8_linear_noalloc keeps its split-K partials in.
+constexpr size_t kQ8ScratchBytes = (size_t)16 << 20;
+// The device address of that scratch on the current device (taken once per device).
+hipError_t q8_scratch_address(float** ptr);
 
 struct TransitionArgs {
   const half_t* z;      // [cells, C]

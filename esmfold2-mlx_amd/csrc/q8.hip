@@ -27,6 +27,8 @@
 // not depend on the order the workgroups ran in. That second kernel is either the
 // reduction here or, for a linear whose output feeds a residual + LayerNorm, the
 // LayerNorm itself (esmc_ln_kernel sums the same partials in the same order).
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -327,6 +329,35 @@ hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N,
   hipLaunchKernelGGL(q8_pack_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st,
                      reinterpret_cast<const uint16_t*>(s), reinterpret_cast<const uint16_t*>(b), sb, N, ngroups, total);
   return hipGetLastError();
+}
+
+// ---- device scratch of the allocation-free entry point -----------------------------------
+// q8_linear_noalloc runs the same plan as q8_linear_ws with its split-K partials in this
+// file-scope array instead of a caller workspace: kQ8ScratchBytes per device, held for the
+// life of the process. On the host, `scratch` names a host-side stand-in, never the device
+// memory: its device address is taken once per device with hipGetSymbolAddress (with that
+// device current) and only that address reaches a kernel. Every split writes all of its
+// partial outputs before the reduction reads them, so nothing needs clearing between calls;
+// calls that overlap in time on one device share the array and race.
+static __device__ __align__(256) float scratch[kQ8ScratchBytes / sizeof(float)];
+
+hipError_t q8_scratch_address(float** ptr) {
+  constexpr int kMaxDev = 64;
+  static std::mutex mu;
+  static float* addr[kMaxDev] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    addr[dev] = static_cast<float*>(p);
+  }
+  *ptr = addr[dev];
+  return hipSuccess;
 }
 
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s) {

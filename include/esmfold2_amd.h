@@ -310,6 +310,21 @@ int distogram_expected_distance(const float* r, const esm_half* w, const float* 
 int abs_diff_quantile(const float* x, const float* y, size_t n, float q, float* out, void* stream);
 
 /*
+ * q8_linear_ws without a workspace, for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops that forbid allocation). No counterpart in the
+ * reference: its MLX quantized_matmul allocates its own outputs. Same plan and same bits
+ * as q8_linear_ws with a workspace; the split-K partials live in a static device array of
+ * ESM_Q8_NOALLOC_SCRATCH_BYTES per GPU (taken by the library for the life of the
+ * process). A shape whose partials exceed it is refused with ESM_ERR_SHAPE (with 256
+ * compute units the plan needs at most about 10.5 MB). Nothing is allocated and nothing
+ * needs clearing between calls; calls that overlap in time on one GPU share the array and
+ * race, so a caller serialises them (one stream, or its own ordering).
+ */
+#define ESM_Q8_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int q8_linear_noalloc(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, const uint32_t* sb,
+                      esm_half* y, int M, int K, int N, int group, void* stream);
+
+/*
  * Quantise fp32 weights to the 8-bit layout q8_linear reads: MLX's affine scheme, group
  * 64 along K, scales and biases rounded to fp16.
  *
