@@ -525,8 +525,8 @@ int esmc_qk_rope(const esm_half* qkv, const float* q_ln, const float* k_ln, floa
 int esmc_attention(const esm_half* q, const esm_half* k, const esm_half* v, const int* sequence_id, esm_half* o, int B,
                    int L, int n_heads, int head_dim, float scale, void* stream) {
   if (B < 0 || L < 0 || n_heads <= 0) return fail(ESM_ERR_SHAPE, "esmc_attention: B=%d L=%d heads=%d", B, L, n_heads);
-  if (head_dim != 64 || L > 512) return fail(ESM_ERR_UNSUPPORTED, "esmc_attention: head_dim=%d L=%d (64, <= 512)",
-                                             head_dim, L);
+  if (head_dim != 64 || L > 65536)
+    return fail(ESM_ERR_UNSUPPORTED, "esmc_attention: head_dim=%d L=%d (64, L <= 65536)", head_dim, L);
   if (B == 0 || L == 0) return ok();
   if ((long long)B * n_heads > 65535) return fail(ESM_ERR_SHAPE, "esmc_attention: B*heads=%d too large", B * n_heads);
   if (!q || !k || !v || !o) return fail(ESM_ERR_NULL, "esmc_attention: NULL pointer");

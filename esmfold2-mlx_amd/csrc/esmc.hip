@@ -195,8 +195,10 @@ __global__ __launch_bounds__(NTR) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
 }
 
 // ---- attention ---------------------------------------------------------------------------------
-// One workgroup = 4 waves = 32 queries of one (batch, head). Wave w takes keys
-// [KW w, KW (w + 1)) (KW = LP / 4): it streams its K and V rows into a private LDS region
+// One workgroup = 4 waves = 32 queries of one (batch, head). Keys go in passes of LP (256
+// or 512; one pass up to L = 512, any length beyond in several, with an online softmax
+// carrying each wave's running max, sum and O across passes). Per pass wave w takes keys
+// [base + KW w, base + KW (w + 1)) (KW = LP / 4): it streams its K and V rows into a private LDS region
 // with buffer loads that write LDS directly, computes S^T = K Q^T for its keys and a
 // softmax partial in fp32 (row max m_w, sum l_w, O_w = P V), and the four partials merge
 // through LDS: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w, M = max_w m_w.
@@ -236,33 +238,14 @@ __global__ __launch_bounds__(256, NKB <= 8 ? 2 : 1) void esmc_attention_kernel(E
   // one XCD and fetch that head's K and V into one L2.
   const int nqb = (p.L + 31) / 32, t = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = t / nqb, b = bh / p.H;
-  const int q0 = (t - bh * nqb) * 32, key0 = KW * wave;
-  const bool live = key0 < L;  // wave-uniform: a wave past the last key only merges
+  const int q0 = (t - bh * nqb) * 32;
   const bool has_sid = p.sid != nullptr;
   char* ks = kv_s[wave];
   char* vs = kv_s[wave] + KW * 128;
-
-  // K, V rows and key ids of this wave's keys; keys past L load zeros (and are masked).
-  if (live) {
-    const rsrc_t rk = make_rsrc_n(p.k + (size_t)bh * L * HD, (uint32_t)L * HD * 2u);
-    const rsrc_t rv = make_rsrc_n(p.v + (size_t)bh * L * HD, (uint32_t)L * HD * 2u);
-#pragma unroll
-    for (int i = 0; i < KW / 8; i++) {
-      const int n = 8 * i + (lane >> 3), lp = lane & 7;  // row n of this wave's keys, LDS piece lp
-      const uint32_t row = (uint32_t)(key0 + n) * 128u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(ks + 1024 * i), 16,
-                                               (int)(row + 16u * (lp ^ ((n >> 1) & 7))), 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(vs + 1024 * i), 16,
-                                               (int)(row + 16u * (lp ^ (((n >> 1) & 1) << 2))), 0, 0, 0);
-    }
-    if (has_sid) {
-      const rsrc_t rs = make_rsrc_n(p.sid + (size_t)b * L, (uint32_t)L * 4u);
-#pragma unroll
-      for (int i = 0; i < KW / 64; i++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(&sid_s[wave][64 * i]),
-                                                 4, (int)((uint32_t)(key0 + 64 * i + lane) * 4u), 0, 0, 0);
-    }
-  }
+  const rsrc_t rk = make_rsrc_n(p.k + (size_t)bh * L * HD, (uint32_t)L * HD * 2u);
+  const rsrc_t rv = make_rsrc_n(p.v + (size_t)bh * L * HD, (uint32_t)L * HD * 2u);
+  const rsrc_t rs = make_rsrc_n(has_sid ? (const void*)(p.sid + (size_t)b * L) : (const void*)p.k,
+                                has_sid ? (uint32_t)L * 4u : 0u);
 
   // Q fragments (B operand: column = query, k = 16 ks + 8 h + e)
   const int qrow = q0 + r;
@@ -271,21 +254,56 @@ __global__ __launch_bounds__(256, NKB <= 8 ? 2 : 1) void esmc_attention_kernel(E
 #pragma unroll
   for (int ks4 = 0; ks4 < HD / 16; ks4++) qf[ks4] = bload16(rq, qrow < L ? (uint32_t)(qrow * HD + 16 * ks4 + 8 * h) * 2u : kOOB);
   const int qsid = has_sid && qrow < L ? p.sid[(size_t)b * L + qrow] : 0;
-  __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0): this wave's LDS rows and Q are in
-  __asm__ volatile("" ::: "memory");
 
-  f32x16 s[KB];
-  float mx = -INFINITY;
-  if (live) {
+  // The keys go in passes of LP (one pass up to L = LP); per pass wave w takes keys
+  // [base + KW w, base + KW (w + 1)), and its running (max, sum, O) are rescaled by
+  // 2^(m_old - m_new) when a later pass raises the max (an online softmax).
+  float m_run = -INFINITY, sum = 0.f;  // sum: this lane's half of the query's running sum
+  f32x16 o[HD / 32];
+#pragma unroll
+  for (int db = 0; db < HD / 32; db++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) o[db][i] = 0.f;
+  for (int base = 0; base < L; base += LP) {
+    const int key0 = base + KW * wave;
+    const bool live = key0 < L;  // wave-uniform: a wave past the last key skips the pass
+    // the previous pass's LDS reads have all returned before its MFMAs ran; keep the
+    // compiler from moving them past the loads that overwrite the rows
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __asm__ volatile("" ::: "memory");
+    // K, V rows and key ids of this wave's keys; keys past L load zeros (and are masked).
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < KW / 8; i++) {
+        const int n = 8 * i + (lane >> 3), lp = lane & 7;  // row n of this wave's keys, LDS piece lp
+        const uint32_t row = (uint32_t)(key0 + n) * 128u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(ks + 1024 * i), 16,
+                                                 (int)(row + 16u * (lp ^ ((n >> 1) & 7))), 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(vs + 1024 * i), 16,
+                                                 (int)(row + 16u * (lp ^ (((n >> 1) & 1) << 2))), 0, 0, 0);
+      }
+      if (has_sid) {
+#pragma unroll
+        for (int i = 0; i < KW / 64; i++)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(&sid_s[wave][64 * i]),
+                                                   4, (int)((uint32_t)(key0 + 64 * i + lane) * 4u), 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0x70 | 0xF00);  // vmcnt(0): this wave's LDS rows (and Q) are in
+    __asm__ volatile("" ::: "memory");
+    if (!live) continue;
+
+    f32x16 sc[KB];
+    float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
 #pragma unroll
-      for (int i = 0; i < 16; i++) s[kb][i] = 0.f;
+      for (int i = 0; i < 16; i++) sc[kb][i] = 0.f;
       const int n = 32 * kb + r;
 #pragma unroll
       for (int ks4 = 0; ks4 < HD / 16; ks4++) {
         const half8 kf = *reinterpret_cast<const half8*>(ks + n * 128 + 16 * ((2 * ks4 + h) ^ ((n >> 1) & 7)));
-        s[kb] = mfma32(kf, qf[ks4], s[kb]);
+        sc[kb] = mfma32(kf, qf[ks4], sc[kb]);
       }
 #pragma unroll
       for (int i4 = 0; i4 < 4; i4++) {
@@ -296,31 +314,31 @@ __global__ __launch_bounds__(256, NKB <= 8 ? 2 : 1) void esmc_attention_kernel(E
         for (int e = 0; e < 4; e++) {
           const int i = 4 * i4 + e;
           const bool ok = key0 + kl + e < L && sid4[e] == qsid;
-          s[kb][i] = ok ? s[kb][i] * p.scale_log2 : -INFINITY;
-          mx = fmaxf(mx, s[kb][i]);
+          sc[kb][i] = ok ? sc[kb][i] * p.scale_log2 : -INFINITY;
+          mx = fmaxf(mx, sc[kb][i]);
         }
       }
     }
-  }
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float mref = mx == -INFINITY ? 0.f : mx;  // no key of this wave is visible to the query
-  float sum = 0.f;
-  half8 pf[2 * KB];
-  f32x16 o[HD / 32];
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float mref = m_new == -INFINITY ? 0.f : m_new;  // no key visible to the query yet
+    const float alpha = exp2f(m_run - mref);              // 0 on the first visible pass
+    sum *= alpha;
 #pragma unroll
-  for (int db = 0; db < HD / 32; db++)
+    for (int db = 0; db < HD / 32; db++)
 #pragma unroll
-    for (int i = 0; i < 16; i++) o[db][i] = 0.f;
-  if (live) {
+      for (int i = 0; i < 16; i++) o[db][i] *= alpha;
+    m_run = m_new;
+    half8 pf[2 * KB];
 #pragma unroll
     for (int kb = 0; kb < KB; kb++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const float e = exp2f(s[kb][i] - mref);
+        const float e = exp2f(sc[kb][i] - mref);
         sum += e;
         pf[2 * kb + (i >> 3)][i & 7] = (half_t)e;
       }
-    // O^T[d][query] = sum over this wave's keys of V^T[d][key] P[key][query]
+    // O^T[d][query] += sum over this wave's keys of V^T[d][key] P[key][query]
     const int n0q = 16 * ((lane >> 4) & 1);  // d offset of this lane's 16-lane group
 #pragma unroll
     for (int j = 0; j < 2 * KB; j++) {
@@ -332,6 +350,7 @@ __global__ __launch_bounds__(256, NKB <= 8 ? 2 : 1) void esmc_attention_kernel(E
       }
     }
   }
+  const float mx = m_run;
   sum += __shfl_xor(sum, 32);
 
   // Partials -> LDS: m, l per query; O_w in accumulator order over this wave's K rows
@@ -407,7 +426,7 @@ hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s) {
 
 hipError_t launch_esmc_attention(const EsmcAttnArgs& a, hipStream_t s) {
   const dim3 grid(((a.L + 31) / 32) * a.B * a.H);
-  if (a.L <= 256)
+  if (a.L <= 256)  // one pass of 256 keys; longer sequences take passes of 512
     hipLaunchKernelGGL(esmc_attention_kernel<8>, grid, dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL(esmc_attention_kernel<16>, grid, dim3(256), 0, s, a);

@@ -265,7 +265,7 @@ int q8_pack_scales(const esm_half* s, const esm_half* b, uint32_t* sb, int N, in
  *   mx.fast.scaled_dot_product_attention), with token i attending to j iff
  *   sequence_id[b, i] == sequence_id[b, j] (:186-191; NULL = no mask); fp32 scores and
  *   softmax, probabilities rounded to fp16 for the second product; o [B, L, H*64] fp16.
- *   head_dim = 64, L <= 512.
+ *   head_dim = 64, L <= 65536 (keys in passes of 512 with an online softmax beyond 512).
  * esmc_swiglu: y = silu(x1) * x2 with x12 = [x1 | x2] rows [M, 2F] fp16 (:100-101), in
  *   fp32, one rounding; y [M, F]. F % 8 == 0.
  */

@@ -58,9 +58,11 @@ def test_qk_rope(gpu_lib, pkg, B, L, H):
     assert torch.equal(v.cpu(), heads(qkv.reshape(B, L, 3 * D)[..., 2 * D:]).contiguous())
 
 
-@pytest.mark.parametrize("L", [1, 5, 31, 64, 130, 238, 300, 512])
+@pytest.mark.parametrize("L", [1, 5, 31, 64, 130, 238, 300, 512, 513, 700, 1100])
 @pytest.mark.parametrize("masked", [False, True])
 def test_attention(gpu_lib, pkg, L, masked):
+    # beyond 512 tokens the keys go in passes of 512 with an online softmax: the chains then
+    # span pass boundaries, and queries of the later chain see no key in the first pass
     B, H = 2, 3
     g = _gen(L + masked)
     q, k, v = (torch.randn(B, H, L, 64, generator=g).half() for _ in range(3))
@@ -74,6 +76,25 @@ def test_attention(gpu_lib, pkg, L, masked):
     ref = ref.transpose(1, 2).reshape(B, L, H * 64)
     err = float((o.double().cpu() - ref).abs().max())
     assert err <= 1e-2 * float(ref.pow(2).mean().sqrt()), err
+
+
+def test_attention_keys_only_in_a_later_pass(gpu_lib, pkg):
+    # L = 1030: tokens 0..599 are chain 0, the rest chain 1, so the chain-1 queries' first
+    # visible key is in the second pass (the running max starts at -inf), and a 1-token chain
+    # at the end sees only itself
+    B, H, L = 1, 2, 1030
+    g = _gen(77)
+    q, k, v = (3 * torch.randn(B, H, L, 64, generator=g).half() for _ in range(3))
+    sid = torch.zeros(B, L, dtype=torch.int32)
+    sid[0, 600:] = 1
+    sid[0, L - 1] = 2
+    o = pkg.kernels.esmc_attention(q.to(DEV), k.to(DEV), v.to(DEV), sid.to(DEV))
+    ref = oe.attention(q.double(), k.double(), v.double(), oe.chain_mask(sid), 0.125)
+    ref = ref.transpose(1, 2).reshape(B, L, H * 64)
+    err = float((o.double().cpu() - ref).abs().max())
+    assert err <= 1e-2 * float(ref.pow(2).mean().sqrt()), err
+    # the lone token's output is its own value row
+    assert torch.allclose(o[0, L - 1].view(H, 64).float().cpu(), v[0, :, L - 1].float(), atol=1e-3)
 
 
 def test_swiglu(gpu_lib, pkg):
@@ -142,6 +163,24 @@ def test_block(gpu_lib, pkg, D, F_, H, L, masked):
         sid[0, 20:] = 1
     rs = math.sqrt(80 / 36)
     out = blk(x.to(DEV), None if sid is None else sid.to(DEV), res_scale=rs).double().cpu()
+    ref = oe.block_forward(p, x.double(), sid, n_heads=H, res_scale=rs, weights="f16")
+    upd = ref - x.double()
+    err = float((out - ref).abs().max())
+    assert err <= 1e-2 * float(upd.pow(2).mean().sqrt()), err
+
+
+def test_block_real_width(gpu_lib, pkg):
+    # the ESMC block at the width the reference runs (D = 2560, 40 heads; FFN 5120), 238 tokens,
+    # two chains: every linear at its real shape (wqkv 2560 -> 7680, wo 2560 -> 2560 split-K,
+    # w1 2560 -> 10240, w2 5120 -> 2560 split-K)
+    D, F_, H, L = 2560, 5120, 40, 238
+    p = _weights(D, F_, seed=5)
+    blk = _module_block(pkg, p, H)
+    x = 2 * torch.randn(1, L, D, generator=_gen(9))
+    sid = torch.zeros(1, L, dtype=torch.int64)
+    sid[0, 150:] = 1
+    rs = math.sqrt(80 / 36)
+    out = blk(x.to(DEV), sid.to(DEV), res_scale=rs).double().cpu()
     ref = oe.block_forward(p, x.double(), sid, n_heads=H, res_scale=rs, weights="f16")
     upd = ref - x.double()
     err = float((out - ref).abs().max())
