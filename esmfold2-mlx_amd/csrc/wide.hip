@@ -166,32 +166,67 @@ __global__ __launch_bounds__(256) void ln_cf_to_cl_kernel(const half_t* __restri
 // ---- the wide GEMM ------------------------------------------------------------------------
 namespace {
 constexpr int WBM = 128;         // cells per tile
-constexpr int WBN = 128;         // outputs per tile
-constexpr int WBK = 32;          // k per stage
-constexpr int WKS = WBK + 8;     // LDS row stride (halfs): 20 dwords
-constexpr int WKC = WBK / 8;     // 16-byte chunks per row per stage
-constexpr int WNT = 256;         // threads
-constexpr int WOS = WBN + 8;     // LDS row stride (halfs) of the staged output tile
+constexpr int WNT = 512;         // threads: 8 waves, two per SIMD
 }  // namespace
 
-template <int EPI, bool DUAL, bool A2SEP>
+// The epilogue value of one output element from its fp32 sums d1 (GEMM 1) and d2 (GEMM 2),
+// before the one rounding to fp16. `in` is false for the padding cells and outputs.
+template <int EPI>
+DEV float wide_value(const WideArgs& p, float d1, float d2, size_t cell, int o, bool in) {
+  float v;
+  if constexpr (EPI == kWideGateCM) {
+    v = d1 * sigmoidf_fast(d2);
+    if (p.mask) v *= in ? (float)p.mask[cell] : 0.f;
+  } else if constexpr (EPI == kWideResGate) {
+    v = d1 * sigmoid_from_t(d2 * kNegLog2e);
+    if (p.mask && p.out_mask) v *= in ? (float)p.mask[cell] : 0.f;
+    if (p.residual) v += in ? (float)p.z[cell * p.ldo + o] : 0.f;
+  } else if constexpr (EPI == kWideRelu) {
+    v = fmaxf(d1, 0.f);
+  } else if constexpr (EPI == kWideSwiglu) {
+    v = d1 * sigmoidf_fast(d1) * d2;
+  } else {  // kWideResid
+    v = d1 + (in ? (float)p.z[cell * p.ldo + o] : 0.f);
+  }
+  return v;
+}
+
+// Eight waves. DUAL (two GEMMs on the same outputs): a tile is 128 cells x 128 outputs;
+// waves 0-3 compute GEMM 1 and waves 4-7 GEMM 2, each wave 64 cells x 64 outputs (2 x 2
+// MFMA tiles, 64 accumulators), so both run at two waves per SIMD; the GEMM-2 waves hand
+// their sums to the GEMM-1 waves through LDS (same wave-tile coordinates, so the same
+// register index of the same lane: conflict-free 16-byte slots). Single GEMM: 128 cells x
+// 256 outputs, 2 x 4 waves. Per stage of BK k: NA A panels of 128 cell rows and 256 weight
+// rows (W1 then W2 for DUAL).
+template <int EPI, bool DUAL, bool A2SEP, int BK>
 __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
-  constexpr int NA = A2SEP ? 2 : 1;          // A panels per stage
-  constexpr int NW = DUAL ? 2 : 1;           // W panels per stage
-  constexpr int STAGE = (NA * WBM + NW * WBN) * WKS;
-  constexpr int SMEM = (2 * STAGE > WBM * WOS) ? 2 * STAGE : WBM * WOS;
-  constexpr int CH_A = WBM * WKC / WNT;      // 16-byte loads per thread per panel
-  constexpr int CH_W = WBN * WKC / WNT;
-  constexpr bool CM = EPI == kWideGateCM;    // channel-major output: D[cell][o]
-  __shared__ __align__(16) half_t smem[SMEM];
+  constexpr int NA = A2SEP ? 2 : 1;            // A panels per stage
+  constexpr int WNW = DUAL ? 2 : 4;            // waves along the outputs per GEMM
+  constexpr int BN = 64 * WNW;                 // outputs per tile
+  constexpr int WROWS = 256;                   // weight rows per stage
+  constexpr int KS = BK + 8;                   // LDS row stride (halfs)
+  constexpr int KC = BK / 8;                   // 16-byte chunks per row per stage
+  constexpr int STAGE = (NA * WBM + WROWS) * KS;
+  constexpr int OS = BN + 8;                   // output staging row stride (halfs)
+  constexpr bool CM = EPI == kWideGateCM;      // channel-major output: D[cell][o]
+  constexpr int OUT_HALFS = CM ? BN * (WBM + 8) : WBM * OS;
+  constexpr int XCH_BYTES = DUAL ? 4 * 64 * 64 * 4 : 0;  // GEMM-2 sums of the 4 waves
+  constexpr int SMEM_BYTES = 2 * STAGE * 2 > OUT_HALFS * 2 + XCH_BYTES ? 2 * STAGE * 2 : OUT_HALFS * 2 + XCH_BYTES;
+  constexpr int CH_A = WBM * KC / WNT;         // 16-byte loads per thread per A panel
+  constexpr int CH_W = WROWS * KC / WNT;
+  static_assert(CH_A >= 1 && CH_W >= 1, "whole loads per thread");
+  __shared__ __align__(16) char smem_c[SMEM_BYTES];
+  half_t* smem = reinterpret_cast<half_t*>(smem_c);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int role = DUAL ? wave >> 2 : 0;                       // which GEMM this wave computes
+  const int wm = DUAL ? (wave >> 1) & 1 : wave >> 2;           // 64-cell half of the tile
+  const int wn = DUAL ? wave & 1 : wave & 3;                   // 64-output block
   const int L = p.L, K = p.K;
-  const int ntn = (p.N + WBN - 1) / WBN;
+  const int ntn = (p.N + BN - 1) / BN;
   const int t = xcd_remap(blockIdx.x, gridDim.x);
-  const int mt = t / ntn, n0 = (t - mt * ntn) * WBN;
+  const int mt = t / ntn, n0 = (t - mt * ntn) * BN;
   const int bl = mt / p.tiles_per_line;      // (batch, line)
   const int pos0 = (mt - bl * p.tiles_per_line) * WBM;
   const int bi = bl / L, line = bl - bi * L;
@@ -202,16 +237,16 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
 
   const rsrc_t rA1 = make_rsrc(p.a1), rA2 = make_rsrc(A2SEP ? p.a2 : p.a1);
   const rsrc_t rW1 = make_rsrc(p.w1 + (size_t)n0 * K), rW2 = make_rsrc((DUAL ? p.w2 : p.w1) + (size_t)n0 * K);
-  const int nk = (K + WBK - 1) / WBK;
+  const int nk = (K + BK - 1) / BK;
 
   struct Regs {
-    half8 a[NA][CH_A], w[NW][CH_W];
+    half8 a[NA][CH_A], w[CH_W];
   };
   auto gload = [&](Regs& r, int kt) {
     const bool live = kt < nk;
 #pragma unroll
     for (int u = 0; u < CH_A; u++) {
-      const int id = tid + WNT * u, row = id / WKC, k = kt * WBK + (id % WKC) * 8;
+      const int id = tid + WNT * u, row = id / KC, k = kt * BK + (id % KC) * 8;
       const bool ok = live && row < nvalid && k < K;
       const uint32_t off = ok ? (uint32_t)((cell0 + (size_t)row * cstride) * K + k) * 2u : kOOB;
       r.a[0][u] = bload16(rA1, off);
@@ -219,10 +254,12 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
     }
 #pragma unroll
     for (int u = 0; u < CH_W; u++) {
-      const int id = tid + WNT * u, row = id / WKC, k = kt * WBK + (id % WKC) * 8;
-      const uint32_t off = live && n0 + row < p.N && k < K ? (uint32_t)(row * K + k) * 2u : kOOB;
-      r.w[0][u] = bload16(rW1, off);
-      if constexpr (DUAL) r.w[1][u] = bload16(rW2, off);
+      const int id = tid + WNT * u, row = id / KC, k = kt * BK + (id % KC) * 8;
+      // DUAL: rows [0, 128) are W1's outputs n0.., rows [128, 256) W2's; else W1's n0 .. n0+255
+      const int n = DUAL ? (row & (BN - 1)) : row;
+      const bool ok = live && n0 + n < p.N && k < K;
+      const uint32_t off = ok ? (uint32_t)(n * K + k) * 2u : kOOB;
+      r.w[u] = bload16(DUAL && row >= BN ? rW2 : rW1, off);
     }
   };
   auto swrite = [&](const Regs& r, int buf) {
@@ -232,51 +269,39 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
 #pragma unroll
       for (int u = 0; u < CH_A; u++) {
         const int id = tid + WNT * u;
-        st16(s + (pa * WBM + id / WKC) * WKS + (id % WKC) * 8, r.a[pa][u]);
+        st16(s + (pa * WBM + id / KC) * KS + (id % KC) * 8, r.a[pa][u]);
       }
 #pragma unroll
-    for (int pw = 0; pw < NW; pw++)
-#pragma unroll
-      for (int u = 0; u < CH_W; u++) {
-        const int id = tid + WNT * u;
-        st16(s + (NA * WBM + pw * WBN + id / WKC) * WKS + (id % WKC) * 8, r.w[pw][u]);
-      }
+    for (int u = 0; u < CH_W; u++) {
+      const int id = tid + WNT * u;
+      st16(s + (NA * WBM + id / KC) * KS + (id % KC) * 8, r.w[u]);
+    }
   };
 
-  f32x16 acc[2][2][2];  // [gemm][mi][ni]
+  f32x16 acc[2][2];  // [mi][ni]
 #pragma unroll
-  for (int g = 0; g < 2; g++)
+  for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-    for (int mi = 0; mi < 2; mi++)
+    for (int ni = 0; ni < 2; ni++)
 #pragma unroll
-      for (int ni = 0; ni < 2; ni++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[g][mi][ni][e] = 0.f;
+      for (int e = 0; e < 16; e++) acc[mi][ni][e] = 0.f;
 
+  const int arow0 = (A2SEP ? role * WBM : 0) + wm * 64;          // this wave's A rows in a stage
+  const int wrow0 = NA * WBM + (DUAL ? role * BN : 0) + wn * 64;  // and its weight rows
   auto compute = [&](int buf) {
     const half_t* s = smem + buf * STAGE;
 #pragma unroll
-    for (int kk = 0; kk < WBK / 16; kk++) {
-      half8 af[NA][2], wf[NW][2];
+    for (int kk = 0; kk < BK / 16; kk++) {
+      half8 af[2], wf[2];
 #pragma unroll
-      for (int pa = 0; pa < NA; pa++)
+      for (int mi = 0; mi < 2; mi++) af[mi] = ld16(s + (arow0 + mi * 32 + (lane & 31)) * KS + kk * 16 + 8 * (lane >> 5));
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++)
-          af[pa][mi] = ld16(s + (pa * WBM + wm * 64 + mi * 32 + (lane & 31)) * WKS + kk * 16 + 8 * (lane >> 5));
+      for (int ni = 0; ni < 2; ni++) wf[ni] = ld16(s + (wrow0 + ni * 32 + (lane & 31)) * KS + kk * 16 + 8 * (lane >> 5));
 #pragma unroll
-      for (int pw = 0; pw < NW; pw++)
+      for (int mi = 0; mi < 2; mi++)
 #pragma unroll
         for (int ni = 0; ni < 2; ni++)
-          wf[pw][ni] = ld16(s + (NA * WBM + pw * WBN + wn * 64 + ni * 32 + (lane & 31)) * WKS + kk * 16 + 8 * (lane >> 5));
-#pragma unroll
-      for (int g = 0; g < (DUAL ? 2 : 1); g++)
-#pragma unroll
-        for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-          for (int ni = 0; ni < 2; ni++) {
-            const half8 a = af[A2SEP ? g : 0][mi], w = wf[g][ni];
-            acc[g][mi][ni] = CM ? mfma32(a, w, acc[g][mi][ni]) : mfma32(w, a, acc[g][mi][ni]);
-          }
+          acc[mi][ni] = CM ? mfma32(af[mi], wf[ni], acc[mi][ni]) : mfma32(wf[ni], af[mi], acc[mi][ni]);
     }
   };
 
@@ -296,71 +321,85 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
     __syncthreads();
   }
 
-  // ---- epilogue: values in fp32, one rounding, staged in LDS ------------------------------
-  // CM:  lane holds output o = lane % 32 (+ tile offsets) and 4 consecutive cells per group;
-  //      staged as [o][cell].
-  // else lane holds cell = lane % 32 and 4 consecutive outputs per group; staged [cell][o].
-  half_t* os = smem;
+  // ---- epilogue ---------------------------------------------------------------------------
+  // DUAL: the GEMM-2 waves store their sums, the GEMM-1 waves read them at the same
+  // (wave tile, register, lane) and compute every value; then all waves stage and store.
+  f32x4* xch = reinterpret_cast<f32x4*>(smem_c + OUT_HALFS * 2);
+  const int wt = wm * WNW + wn;  // wave-tile index within one GEMM
+  if (DUAL && role == 1) {
 #pragma unroll
-  for (int mi = 0; mi < 2; mi++)
+    for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-    for (int ni = 0; ni < 2; ni++)
+      for (int ni = 0; ni < 2; ni++)
 #pragma unroll
-      for (int g4 = 0; g4 < 4; g4++) {
-        const int rq = acc_row32(4 * g4, lane);                      // first of 4 consecutive
-        const int cl = CM ? wm * 64 + mi * 32 + rq : wm * 64 + mi * 32 + (lane & 31);
-        const int ol = CM ? wn * 64 + ni * 32 + (lane & 31) : wn * 64 + ni * 32 + rq;
-        half4 hv;
+        for (int g4 = 0; g4 < 4; g4++)
+          xch[((wt * 4 + mi * 2 + ni) * 4 + g4) * 64 + lane] =
+              f32x4{acc[mi][ni][4 * g4], acc[mi][ni][4 * g4 + 1], acc[mi][ni][4 * g4 + 2], acc[mi][ni][4 * g4 + 3]};
+  }
+  __syncthreads();
+  // CM: lane holds output o = lane % 32 (+ tile offsets) and 4 consecutive cells per group;
+  //     staged as [o][cell]. Else lane holds cell = lane % 32 and 4 consecutive outputs per
+  //     group; staged as [cell][o].
+  half4 hv[2][2][4];
+  if (role == 0) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int c_e = CM ? cl + e : cl, o_e = CM ? ol : ol + e;  // this value's cell and output
-          const float d1 = acc[0][mi][ni][4 * g4 + e];
-          const float d2 = DUAL ? acc[1][mi][ni][4 * g4 + e] : 0.f;
-          const bool cin = c_e < nvalid && n0 + o_e < p.N;
-          const size_t cell = cell0 + (size_t)c_e * cstride;
-          float v;
-          if constexpr (EPI == kWideGateCM) {
-            v = d1 * sigmoidf_fast(d2);
-            if (p.mask) v *= cin ? (float)p.mask[cell] : 0.f;
-          } else if constexpr (EPI == kWideResGate) {
-            v = d1 * sigmoid_from_t(d2 * kNegLog2e);
-            if (p.mask && p.out_mask) v *= cin ? (float)p.mask[cell] : 0.f;
-            if (p.residual) v += cin ? (float)p.z[cell * p.ldo + n0 + o_e] : 0.f;
-          } else if constexpr (EPI == kWideRelu) {
-            v = fmaxf(d1, 0.f);
-          } else if constexpr (EPI == kWideSwiglu) {
-            v = d1 * sigmoidf_fast(d1) * d2;
-          } else {  // kWideResid
-            v = d1 + (cin ? (float)p.z[cell * p.ldo + n0 + o_e] : 0.f);
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+          const int rq = acc_row32(4 * g4, lane);
+          const int cl = CM ? wm * 64 + mi * 32 + rq : wm * 64 + mi * 32 + (lane & 31);
+          const int ol = CM ? wn * 64 + ni * 32 + (lane & 31) : wn * 64 + ni * 32 + rq;
+          f32x4 d2 = {0.f, 0.f, 0.f, 0.f};
+          if (DUAL) d2 = xch[((wt * 4 + mi * 2 + ni) * 4 + g4) * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int c_e = CM ? cl + e : cl, o_e = CM ? ol : ol + e;
+            const bool in = c_e < nvalid && n0 + o_e < p.N;
+            hv[mi][ni][g4][e] = (half_t)wide_value<EPI>(p, acc[mi][ni][4 * g4 + e], d2[e],
+                                                        cell0 + (size_t)c_e * cstride, n0 + o_e, in);
           }
-          hv[e] = (half_t)v;
         }
-        if (CM) {
-          *reinterpret_cast<half4*>(os + ol * WOS + cl) = hv;  // [o][cell .. cell+3]
-        } else {
-          *reinterpret_cast<half4*>(os + cl * WOS + ol) = hv;  // [cell][o .. o+3]
+  }
+  __syncthreads();  // the exchange area is free again
+  half_t* os = smem;
+  if (role == 0) {
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+          const int rq = acc_row32(4 * g4, lane);
+          const int cl = CM ? wm * 64 + mi * 32 + rq : wm * 64 + mi * 32 + (lane & 31);
+          const int ol = CM ? wn * 64 + ni * 32 + (lane & 31) : wn * 64 + ni * 32 + rq;
+          if (CM)
+            *reinterpret_cast<half4*>(os + ol * (WBM + 8) + cl) = hv[mi][ni][g4];  // [o][cell .. cell+3]
+          else
+            *reinterpret_cast<half4*>(os + cl * OS + ol) = hv[mi][ni][g4];         // [cell][o .. o+3]
         }
-      }
+  }
   __syncthreads();
   if constexpr (CM) {
     // channel rows: output o -> plane a (o < c) or b, channel (n0 + o) % c; positions
     // pos0 .. pos0+127 of row `line`, up to ld (the padding columns get the zeros computed
     // for the cells past L).
 #pragma unroll
-    for (int u = 0; u < WBN * (WBM / 8) / WNT; u++) {
+    for (int u = 0; u < BN * (WBM / 8) / WNT; u++) {
       const int id = tid + WNT * u, o = id / (WBM / 8), q = id - o * (WBM / 8);
       const int n = n0 + o;
       if (n >= p.N || pos0 + 8 * q >= p.ld) continue;
       half_t* plane = n < p.c ? p.plane_a : p.plane_b;
       const int ch = n < p.c ? n : n - p.c;
-      st16(plane + (((size_t)bi * p.c + ch) * L + line) * p.ld + pos0 + 8 * q, ld16(os + o * WOS + 8 * q));
+      st16(plane + (((size_t)bi * p.c + ch) * L + line) * p.ld + pos0 + 8 * q, ld16(os + o * (WBM + 8) + 8 * q));
     }
   } else {
 #pragma unroll
-    for (int u = 0; u < WBM * (WBN / 8) / WNT; u++) {
-      const int id = tid + WNT * u, c2 = id / (WBN / 8), q = id - c2 * (WBN / 8);
+    for (int u = 0; u < WBM * (BN / 8) / WNT; u++) {
+      const int id = tid + WNT * u, c2 = id / (BN / 8), q = id - c2 * (BN / 8);
       if (c2 >= nvalid || n0 + 8 * q >= p.N) continue;
-      st16(p.out + (cell0 + (size_t)c2 * cstride) * p.ldo + n0 + 8 * q, ld16(os + c2 * WOS + 8 * q));
+      st16(p.out + (cell0 + (size_t)c2 * cstride) * p.ldo + n0 + 8 * q, ld16(os + c2 * OS + 8 * q));
     }
   }
 }
@@ -413,8 +452,11 @@ hipError_t launch_ln_cf_to_cl(const half_t* x, int ldx, const float* w, const fl
 }
 
 long long wide_gemm_blocks(const WideArgs& a) {
-  return (long long)a.B * a.L * a.tiles_per_line * ((a.N + WBN - 1) / WBN);
+  const int bn = a.w2 != nullptr ? 128 : 256;
+  return (long long)a.B * a.L * a.tiles_per_line * ((a.N + bn - 1) / bn);
 }
+
+constexpr int kWideBK = 64;
 
 hipError_t launch_wide_gemm(const WideArgs& a, int epi, hipStream_t s) {
   const dim3 grid((unsigned)wide_gemm_blocks(a)), block(WNT);
@@ -422,23 +464,23 @@ hipError_t launch_wide_gemm(const WideArgs& a, int epi, hipStream_t s) {
   switch (epi) {
     case kWideGateCM:
       if (!dual || sep) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideGateCM, true, false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((wide_gemm_kernel<kWideGateCM, true, false, kWideBK>), grid, block, 0, s, a);
       break;
     case kWideResGate:
       if (!dual || !sep) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideResGate, true, true>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((wide_gemm_kernel<kWideResGate, true, true, kWideBK>), grid, block, 0, s, a);
       break;
     case kWideRelu:
       if (dual) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideRelu, false, false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((wide_gemm_kernel<kWideRelu, false, false, kWideBK>), grid, block, 0, s, a);
       break;
     case kWideSwiglu:
       if (!dual || sep) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideSwiglu, true, false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((wide_gemm_kernel<kWideSwiglu, true, false, kWideBK>), grid, block, 0, s, a);
       break;
     case kWideResid:
       if (dual) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideResid, false, false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((wide_gemm_kernel<kWideResid, false, false, kWideBK>), grid, block, 0, s, a);
       break;
     default:
       return hipErrorInvalidValue;
