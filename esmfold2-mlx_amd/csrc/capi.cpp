@@ -221,7 +221,7 @@ static int tmu_forward_wide(const esm_half* z, const esm_half* mask, const float
   g.c = c;
   g.ld = ld;
   if (esm::wide_gemm_blocks(g) > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_forward: too many tiles");
-  e = esm::launch_wide_gemm(g, esm::kWideGateCM, st);
+  e = esm::launch_wide_gemm(g, esm::kWideGateCM, st, cu_count());
   if (e != hipSuccess) return hip_status(e, "tmu_forward gate launch");
   esm::ContractArgs ca{wa, wb, wx, B * c, L, ld, ld, kScale};
   e = esm::launch_contract(ca, st);
@@ -244,7 +244,7 @@ static int tmu_forward_wide(const esm_half* z, const esm_half* mask, const float
   r.residual = residual ? 1 : 0;
   r.mask = mask ? H(mask) : nullptr;
   r.out_mask = out_mask ? 1 : 0;
-  e = esm::launch_wide_gemm(r, esm::kWideResGate, st);
+  e = esm::launch_wide_gemm(r, esm::kWideResGate, st, cu_count());
   return hip_status(e, "tmu_forward emit launch");
 }
 
@@ -452,7 +452,7 @@ int pair_transition_ws(const esm_half* z, esm_half* out, const float* ln_w, cons
   g.out = wh;
   g.ldo = hidden;
   if (esm::wide_gemm_blocks(g) > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "pair_transition: too many tiles");
-  e = esm::launch_wide_gemm(g, w2 ? esm::kWideSwiglu : esm::kWideRelu, st);
+  e = esm::launch_wide_gemm(g, w2 ? esm::kWideSwiglu : esm::kWideRelu, st, cu_count());
   if (e != hipSuccess) return hip_status(e, "pair_transition hidden launch");
   esm::WideArgs r{};
   r.a1 = wh;
@@ -465,7 +465,7 @@ int pair_transition_ws(const esm_half* z, esm_half* out, const float* ln_w, cons
   r.out = H(out);
   r.ldo = C;
   r.z = H(z);
-  e = esm::launch_wide_gemm(r, esm::kWideResid, st);
+  e = esm::launch_wide_gemm(r, esm::kWideResid, st, cu_count());
   return hip_status(e, "pair_transition output launch");
 }
 

@@ -196,7 +196,9 @@ hipError_t launch_ln_rows(const void* x, const float* x2, bool in_f32, const flo
 hipError_t launch_ln_cf_to_cl(const half_t* x, int ldx, const float* w, const float* b, float eps, half_t* y, int B,
                               int L, int c, hipStream_t s);
 long long wide_gemm_blocks(const WideArgs& a);
-hipError_t launch_wide_gemm(const WideArgs& a, int epi, hipStream_t s);
+// cus > 0 with K = 128 or 256: the weight-stationary persistent form (one workgroup per CU);
+// otherwise the streaming tiled form.
+hipError_t launch_wide_gemm(const WideArgs& a, int epi, hipStream_t s, int cus);
 hipError_t launch_q8_quantize(const float* w, uint8_t* q, half_t* s, half_t* b, int N, int K, hipStream_t st);
 hipError_t launch_q8_dequant(const uint8_t* q, const half_t* s, const half_t* b, half_t* w, int N, int K,
                              hipStream_t st);

@@ -171,8 +171,9 @@ constexpr int WNT = 512;         // threads: 8 waves, two per SIMD
 
 // The epilogue value of one output element from its fp32 sums d1 (GEMM 1) and d2 (GEMM 2),
 // before the one rounding to fp16. `in` is false for the padding cells and outputs.
+// zv is the residual z[cell][o] (RESGATE with residual, RESID; 0 for the padding).
 template <int EPI>
-DEV float wide_value(const WideArgs& p, float d1, float d2, size_t cell, int o, bool in) {
+DEV float wide_value(const WideArgs& p, float d1, float d2, size_t cell, bool in, float zv) {
   float v;
   if constexpr (EPI == kWideGateCM) {
     v = d1 * sigmoidf_fast(d2);
@@ -180,16 +181,18 @@ DEV float wide_value(const WideArgs& p, float d1, float d2, size_t cell, int o, 
   } else if constexpr (EPI == kWideResGate) {
     v = d1 * sigmoid_from_t(d2 * kNegLog2e);
     if (p.mask && p.out_mask) v *= in ? (float)p.mask[cell] : 0.f;
-    if (p.residual) v += in ? (float)p.z[cell * p.ldo + o] : 0.f;
+    if (p.residual) v += zv;
   } else if constexpr (EPI == kWideRelu) {
     v = fmaxf(d1, 0.f);
   } else if constexpr (EPI == kWideSwiglu) {
     v = d1 * sigmoidf_fast(d1) * d2;
   } else {  // kWideResid
-    v = d1 + (in ? (float)p.z[cell * p.ldo + o] : 0.f);
+    v = d1 + zv;
   }
   return v;
 }
+template <int EPI>
+constexpr bool wide_needs_z() { return EPI == kWideResGate || EPI == kWideResid; }
 
 // Eight waves. DUAL (two GEMMs on the same outputs): a tile is 128 cells x 128 outputs;
 // waves 0-3 compute GEMM 1 and waves 4-7 GEMM 2, each wave 64 cells x 64 outputs (2 x 2
@@ -357,8 +360,10 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
           for (int e = 0; e < 4; e++) {
             const int c_e = CM ? cl + e : cl, o_e = CM ? ol : ol + e;
             const bool in = c_e < nvalid && n0 + o_e < p.N;
-            hv[mi][ni][g4][e] = (half_t)wide_value<EPI>(p, acc[mi][ni][4 * g4 + e], d2[e],
-                                                        cell0 + (size_t)c_e * cstride, n0 + o_e, in);
+            const size_t cell = cell0 + (size_t)c_e * cstride;
+            const float zv = wide_needs_z<EPI>() && in && (EPI == kWideResid || p.residual)
+                                 ? (float)p.z[cell * p.ldo + n0 + o_e] : 0.f;
+            hv[mi][ni][g4][e] = (half_t)wide_value<EPI>(p, acc[mi][ni][4 * g4 + e], d2[e], cell, in, zv);
           }
         }
   }
@@ -401,6 +406,217 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
       if (c2 >= nvalid || n0 + 8 * q >= p.N) continue;
       st16(p.out + (cell0 + (size_t)c2 * cstride) * p.ldo + n0 + 8 * q, ld16(os + c2 * OS + 8 * q));
     }
+  }
+}
+
+// ---- the weight-stationary wide GEMM (K <= 256) --------------------------------------------
+// Persistent: every workgroup owns a slice of 256 weight rows (DUAL: 128 outputs of W1 and
+// the same 128 of W2; single: 256 outputs of W1), held for the whole launch as MFMA
+// fragments in registers (wave w: 32 rows x K, K / 2 registers), and walks tiles of 64
+// cells of one line; only the A tiles stream, through LDS, the next tile's loads in flight
+// while this one is multiplied. A tile is read by the S workgroups of the S slices, which are
+// neighbours in the XCD-aware order (one L2 fetch). Waves 0-3 of a DUAL slice take GEMM 1
+// and 4-7 GEMM 2 for the same outputs; GEMM 2's sums reach GEMM 1's waves through LDS at the
+// same (block, register, lane). Same arithmetic, same order of the K sums, same bits as
+// wide_gemm_kernel.
+namespace {
+constexpr int SBM = 64;   // cells per tile
+}  // namespace
+
+template <int EPI, bool DUAL, bool A2SEP, int KW>  // KW = K / 16
+__global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
+  constexpr int K = 16 * KW;
+  constexpr int NA = A2SEP ? 2 : 1;
+  constexpr int BN = DUAL ? 128 : 256;          // outputs per slice
+  constexpr int AS = K + 8;                     // LDS row stride (halfs) of an A tile
+  constexpr int A_HALFS = NA * SBM * AS;
+  constexpr bool CM = EPI == kWideGateCM;
+  constexpr int OS = CM ? SBM + 8 : BN + 8;     // staging row stride: [o][cell] or [cell][o]
+  constexpr int OUT_HALFS = CM ? BN * OS : SBM * OS;
+  constexpr int XCH_BYTES = DUAL ? 4 * 2 * 4 * 64 * 16 : 0;
+  constexpr int WST_HALFS = 64 * AS;            // start-up: 64 weight rows at a time
+  constexpr int MAIN_BYTES = A_HALFS * 2 + XCH_BYTES + OUT_HALFS * 2;
+  constexpr int SMEM_BYTES = MAIN_BYTES > WST_HALFS * 2 ? MAIN_BYTES : WST_HALFS * 2;
+  constexpr int CH_A = SBM * (K / 8) / WNT;     // 16-byte loads per thread per A tile
+  static_assert(CH_A >= 1 && SBM * (K / 8) % WNT == 0, "whole loads per thread");
+  __shared__ __align__(16) char smem_c[SMEM_BYTES];
+  half_t* a_s = reinterpret_cast<half_t*>(smem_c);
+  f32x4* xch = reinterpret_cast<f32x4*>(smem_c + A_HALFS * 2);
+  half_t* os = reinterpret_cast<half_t*>(smem_c + A_HALFS * 2 + XCH_BYTES);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int role = DUAL ? wave >> 2 : 0;
+  const int wc = DUAL ? wave & 3 : wave;        // 32-output block of this wave
+  const int L = p.L;
+  const int S = (p.N + BN - 1) / BN;            // slices
+  const int lg = xcd_remap(blockIdx.x, gridDim.x);
+  const int slice = lg % S;
+  const int n0 = slice * BN;
+  const int stride = gridDim.x / S;             // tile groups
+  const int tpl = (L + SBM - 1) / SBM;
+  const int ntiles = p.B * L * tpl;
+
+  // weights: rows n0 + 32 wc + r of W1 (role 0) or W2 (role 1), staged 64 rows at a time
+  half8 wf[KW];
+  {
+    const half_t* wsrc[2] = {p.w1, DUAL ? p.w2 : p.w1};
+    for (int r0 = 0; r0 < (DUAL ? 2 * BN : BN); r0 += 64) {
+      // rows r0 .. r0+63 of the slice's row list (DUAL: W1's 128, then W2's 128)
+      for (int q = tid; q < 64 * (K / 8); q += WNT) {
+        const int rr = q / (K / 8), j = q - rr * (K / 8);
+        const int sr = r0 + rr;                              // slice row
+        const int g = DUAL ? sr / BN : 0, n = DUAL ? sr - g * BN : sr;
+        const bool ok = n0 + n < p.N;
+        st16(a_s + rr * AS + 8 * j, ok ? ld16(wsrc[g] + (size_t)(n0 + n) * K + 8 * j) : zero_half8());
+      }
+      __syncthreads();
+      const int my0 = (DUAL ? role * BN : 0) + 32 * wc;    // this wave's first slice row
+      if (my0 >= r0 && my0 < r0 + 64) {
+#pragma unroll
+        for (int kk = 0; kk < KW; kk++) wf[kk] = ld16(a_s + (my0 - r0 + (lane & 31)) * AS + 16 * kk + 8 * (lane >> 5));
+      }
+      __syncthreads();
+    }
+  }
+
+  const rsrc_t rA1 = make_rsrc(p.a1), rA2 = make_rsrc(A2SEP ? p.a2 : p.a1);
+  const rsrc_t rZ = make_rsrc(wide_needs_z<EPI>() ? (const void*)p.z : (const void*)p.a1);
+  constexpr bool ZR = wide_needs_z<EPI>();      // the residual comes in with the A tile
+  auto tile_coords = [&](int tile, int& bi, int& line, int& pos0) {
+    const int bl = tile / tpl;
+    pos0 = (tile - bl * tpl) * SBM;
+    bi = bl / L;
+    line = bl - bi * L;
+  };
+  auto cell_of = [&](int bi, int line, int pos) -> size_t {
+    return p.transpose ? ((size_t)bi * L + pos) * L + line : ((size_t)bi * L + line) * L + pos;
+  };
+  struct Regs {
+    half8 a[NA][CH_A];
+    half4 z[ZR ? 2 : 1][ZR ? 4 : 1];            // role 0: z[cell][4 outputs] per (mi, group)
+  };
+  // One tile's loads: the A rows (every thread), and for the GEMM-1 waves the residual pieces
+  // they add: lane (cell mi*32 + lane%32, outputs 32 wc + acc_row32(4 g4) .. +3), 8 bytes each.
+  auto gload = [&](Regs& r, int tile) {
+    const bool live = tile < ntiles;
+    int bi, line, pos0;
+    tile_coords(live ? tile : 0, bi, line, pos0);
+#pragma unroll
+    for (int u = 0; u < CH_A; u++) {
+      const int id = tid + WNT * u, row = id / (K / 8), j = id - row * (K / 8);
+      const bool ok = live && pos0 + row < L;
+      const uint32_t off = ok ? (uint32_t)(cell_of(bi, line, pos0 + row) * K + 8 * j) * 2u : kOOB;
+      r.a[0][u] = bload16(rA1, off);
+      if constexpr (A2SEP) r.a[1][u] = bload16(rA2, off);
+    }
+    if constexpr (ZR) {
+      const bool want = role == 0 && (EPI == kWideResid || p.residual);
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+          const int c = mi * 32 + (lane & 31), o = n0 + 32 * wc + acc_row32(4 * g4, lane);
+          const bool ok = want && live && pos0 + c < L && o < p.N;
+          const uint32_t off = ok ? (uint32_t)(cell_of(bi, line, pos0 + c) * p.ldo + o) * 2u : kOOB;
+          r.z[mi][g4] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(rZ, (int)off, 0, 0));
+        }
+    }
+  };
+
+  // one tile: A tiles to LDS, the MFMAs, the exchange, the epilogue, the stores
+  auto run_tile = [&](int tile, const Regs& ra) {
+    int bi, line, pos0;
+    tile_coords(tile, bi, line, pos0);
+    const int nvalid = L - pos0;
+#pragma unroll
+    for (int pa = 0; pa < NA; pa++)
+#pragma unroll
+      for (int u = 0; u < CH_A; u++) {
+        const int id = tid + WNT * u, row = id / (K / 8), j = id - row * (K / 8);
+        st16(a_s + (pa * SBM + row) * AS + 8 * j, ra.a[pa][u]);
+      }
+    __syncthreads();
+    // D over this wave's 32 outputs and the tile's 64 cells: 2 chains of KW MFMAs
+    f32x16 acc[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[mi][e] = 0.f;
+    const half_t* at = a_s + (A2SEP ? role * SBM : 0) * AS;
+#pragma unroll
+    for (int kk = 0; kk < KW; kk++)
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++) {
+        const half8 af = ld16(at + (mi * 32 + (lane & 31)) * AS + 16 * kk + 8 * (lane >> 5));
+        acc[mi] = CM ? mfma32(af, wf[kk], acc[mi]) : mfma32(wf[kk], af, acc[mi]);
+      }
+    if (DUAL && role == 1) {
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++)
+          xch[((wc * 2 + mi) * 4 + g4) * 64 + lane] =
+              f32x4{acc[mi][4 * g4], acc[mi][4 * g4 + 1], acc[mi][4 * g4 + 2], acc[mi][4 * g4 + 3]};
+    }
+    __syncthreads();  // the exchange is visible and every wave is done with the A tiles
+    if (role == 0) {
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+          const int rq = acc_row32(4 * g4, lane);
+          const int cl = CM ? mi * 32 + rq : mi * 32 + (lane & 31);  // first cell (CM: of 4)
+          const int ol = CM ? 32 * wc + (lane & 31) : 32 * wc + rq;  // first output (else: of 4)
+          f32x4 d2 = {0.f, 0.f, 0.f, 0.f};
+          if (DUAL) d2 = xch[((wc * 2 + mi) * 4 + g4) * 64 + lane];
+          half4 hv;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int c_e = CM ? cl + e : cl, o_e = CM ? ol : ol + e;
+            const bool in = c_e < nvalid && n0 + o_e < p.N;
+            const float zv = ZR ? (float)ra.z[ZR ? mi : 0][ZR ? g4 : 0][e] : 0.f;  // zeros past the ends
+            hv[e] = (half_t)wide_value<EPI>(p, acc[mi][4 * g4 + e], d2[e], cell_of(bi, line, pos0 + c_e), in, zv);
+          }
+          if (CM)
+            *reinterpret_cast<half4*>(os + ol * OS + cl) = hv;
+          else
+            *reinterpret_cast<half4*>(os + cl * OS + ol) = hv;
+        }
+    }
+    __syncthreads();  // the staged tile is complete
+    if constexpr (CM) {
+      for (int id = tid; id < BN * (SBM / 8); id += WNT) {
+        const int o = id / (SBM / 8), q = id - o * (SBM / 8);
+        const int n = n0 + o;
+        if (n >= p.N || pos0 + 8 * q >= p.ld) continue;
+        half_t* plane = n < p.c ? p.plane_a : p.plane_b;
+        const int ch = n < p.c ? n : n - p.c;
+        st16(plane + (((size_t)bi * p.c + ch) * L + line) * p.ld + pos0 + 8 * q, ld16(os + o * OS + 8 * q));
+      }
+    } else {
+      for (int id = tid; id < SBM * (BN / 8); id += WNT) {
+        const int c2 = id / (BN / 8), q = id - c2 * (BN / 8);
+        if (c2 >= nvalid || n0 + 8 * q >= p.N) continue;
+        st16(p.out + cell_of(bi, line, pos0 + c2) * p.ldo + n0 + 8 * q, ld16(os + c2 * OS + 8 * q));
+      }
+    }
+  };
+
+  // Two tiles' loads in flight: a tile's registers are reloaded (two tiles ahead) only after
+  // its epilogue has used them. Tiles of the next iteration wait for loads issued before
+  // this tile's stores, so the stores never hold them up. The A tiles are rewritten only
+  // after the barriers that end the previous tile's reads of them, the exchange and the
+  // staging area are separate, and the next tile's second barrier orders the staging reuse.
+  const int tg = lg / S;
+  Regs r0, r1;
+  gload(r0, tg);
+  gload(r1, tg + stride);
+  for (int tile = tg; tile < ntiles; tile += 2 * stride) {
+    run_tile(tile, r0);
+    gload(r0, tile + 2 * stride);
+    if (tile + stride < ntiles) run_tile(tile + stride, r1);
+    gload(r1, tile + 3 * stride);
   }
 }
 
@@ -458,7 +674,52 @@ long long wide_gemm_blocks(const WideArgs& a) {
 
 constexpr int kWideBK = 64;
 
-hipError_t launch_wide_gemm(const WideArgs& a, int epi, hipStream_t s) {
+// The weight-stationary form for K = 128 or 256: a persistent grid of whole slice groups.
+static hipError_t launch_wide_gemm_ws(const WideArgs& a, int epi, int cus, hipStream_t s) {
+  const bool dual = a.w2 != nullptr, sep = a.a2 != nullptr && a.a2 != a.a1;
+  const int bn = dual ? 128 : 256;
+  const int S = (a.N + bn - 1) / bn;
+  const long long tiles = (long long)a.B * a.L * ((a.L + SBM - 1) / SBM);
+  long long groups = (cus > S ? cus : S) / S;   // one workgroup per CU
+  groups -= groups % kNumXcd == 0 || groups < kNumXcd ? 0 : groups % kNumXcd;
+  if (groups > tiles) groups = tiles;
+  const dim3 grid((unsigned)(groups * S)), block(WNT);
+#define WS_CASES(KW)                                                                                          \
+  switch (epi) {                                                                                             \
+    case kWideGateCM:                                                                                        \
+      if (!dual || sep) return hipErrorInvalidValue;                                                         \
+      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideGateCM, true, false, KW>), grid, block, 0, s, a);         \
+      break;                                                                                                 \
+    case kWideResGate:                                                                                       \
+      if (!dual || !sep) return hipErrorInvalidValue;                                                        \
+      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideResGate, true, true, KW>), grid, block, 0, s, a);         \
+      break;                                                                                                 \
+    case kWideRelu:                                                                                          \
+      if (dual) return hipErrorInvalidValue;                                                                 \
+      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideRelu, false, false, KW>), grid, block, 0, s, a);          \
+      break;                                                                                                 \
+    case kWideSwiglu:                                                                                        \
+      if (!dual || sep) return hipErrorInvalidValue;                                                         \
+      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideSwiglu, true, false, KW>), grid, block, 0, s, a);         \
+      break;                                                                                                 \
+    case kWideResid:                                                                                         \
+      if (dual) return hipErrorInvalidValue;                                                                 \
+      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideResid, false, false, KW>), grid, block, 0, s, a);         \
+      break;                                                                                                 \
+    default:                                                                                                 \
+      return hipErrorInvalidValue;                                                                           \
+  }
+  if (a.K == 128) {
+    WS_CASES(8)
+  } else {
+    WS_CASES(16)
+  }
+#undef WS_CASES
+  return hipGetLastError();
+}
+
+hipError_t launch_wide_gemm(const WideArgs& a, int epi, hipStream_t s, int cus) {
+  if ((a.K == 128 || a.K == 256) && cus > 0) return launch_wide_gemm_ws(a, epi, cus, s);
   const dim3 grid((unsigned)wide_gemm_blocks(a)), block(WNT);
   const bool dual = a.w2 != nullptr, sep = a.a2 != nullptr && a.a2 != a.a1;
   switch (epi) {

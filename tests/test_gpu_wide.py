@@ -98,7 +98,7 @@ def test_tmu_pair_256_full_size(gpu_lib, pkg):
 
 
 @pytest.mark.parametrize("C,H,swiglu", [(256, 512, True), (256, 1024, True), (256, 1024, False), (128, 512, True),
-                                        (384, 768, True)])
+                                        (384, 768, True), (256, 256, False), (256, 128, True), (512, 256, False)])
 def test_transition_wide_matches_oracle(gpu_lib, pkg, C, H, swiglu):
     g = torch.Generator().manual_seed(C + H)
     L, B = 37, 2
