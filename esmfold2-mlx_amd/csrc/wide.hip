@@ -194,6 +194,35 @@ DEV float wide_value(const WideArgs& p, float d1, float d2, size_t cell, bool in
 template <int EPI>
 constexpr bool wide_needs_z() { return EPI == kWideResGate || EPI == kWideResid; }
 
+// The weight-stationary kernel splits a dual epilogue between its two GEMMs' waves: the
+// waves of the activated GEMM apply the activation to their own accumulators (wide_act)
+// and pass it through LDS, the other waves finish the output (wide_combine). The operations
+// and their order are those of wide_value, so both kernels give the same bits. For SwiGLU
+// the activated GEMM is the first (silu(d1)), so its waves are the ones that pass.
+template <int EPI>
+DEV float wide_act(float d) {
+  if constexpr (EPI == kWideGateCM) return sigmoidf_fast(d);
+  else if constexpr (EPI == kWideResGate) return sigmoid_from_t(d * kNegLog2e);
+  else return d * sigmoidf_fast(d);  // kWideSwiglu: silu(d1)
+}
+template <int EPI>
+DEV float wide_combine(const WideArgs& p, float d, float s, size_t cell, bool in, float zv) {
+  float v;
+  if constexpr (EPI == kWideGateCM) {
+    v = d * s;
+    if (p.mask) v *= in ? (float)p.mask[cell] : 0.f;
+  } else if constexpr (EPI == kWideResGate) {
+    v = d * s;
+    if (p.mask && p.out_mask) v *= in ? (float)p.mask[cell] : 0.f;
+    if (p.residual) v += zv;
+  } else if constexpr (EPI == kWideSwiglu) {
+    v = s * d;                          // silu(d1) * d2
+  } else {
+    v = wide_value<EPI>(p, d, 0.f, cell, in, zv);
+  }
+  return v;
+}
+
 // Eight waves. DUAL (two GEMMs on the same outputs): a tile is 128 cells x 128 outputs;
 // waves 0-3 compute GEMM 1 and waves 4-7 GEMM 2, each wave 64 cells x 64 outputs (2 x 2
 // MFMA tiles, 64 accumulators), so both run at two waves per SIMD; the GEMM-2 waves hand
@@ -457,33 +486,12 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   const int tpl = (L + SBM - 1) / SBM;
   const int ntiles = p.B * L * tpl;
 
-  // weights: rows n0 + 32 wc + r of W1 (role 0) or W2 (role 1), staged 64 rows at a time
-  half8 wf[KW];
-  {
-    const half_t* wsrc[2] = {p.w1, DUAL ? p.w2 : p.w1};
-    for (int r0 = 0; r0 < (DUAL ? 2 * BN : BN); r0 += 64) {
-      // rows r0 .. r0+63 of the slice's row list (DUAL: W1's 128, then W2's 128)
-      for (int q = tid; q < 64 * (K / 8); q += WNT) {
-        const int rr = q / (K / 8), j = q - rr * (K / 8);
-        const int sr = r0 + rr;                              // slice row
-        const int g = DUAL ? sr / BN : 0, n = DUAL ? sr - g * BN : sr;
-        const bool ok = n0 + n < p.N;
-        st16(a_s + rr * AS + 8 * j, ok ? ld16(wsrc[g] + (size_t)(n0 + n) * K + 8 * j) : zero_half8());
-      }
-      __syncthreads();
-      const int my0 = (DUAL ? role * BN : 0) + 32 * wc;    // this wave's first slice row
-      if (my0 >= r0 && my0 < r0 + 64) {
-#pragma unroll
-        for (int kk = 0; kk < KW; kk++) wf[kk] = ld16(a_s + (my0 - r0 + (lane & 31)) * AS + 16 * kk + 8 * (lane >> 5));
-      }
-      __syncthreads();
-    }
-  }
-
+  half8 wf[KW];  // this wave's 32 weight rows as MFMA fragments, for the whole launch
   const rsrc_t rA1 = make_rsrc(p.a1), rA2 = make_rsrc(A2SEP ? p.a2 : p.a1);
   const rsrc_t rZ = make_rsrc(wide_needs_z<EPI>() ? (const void*)p.z : (const void*)p.a1);
   constexpr bool ZR = wide_needs_z<EPI>();      // the residual comes in with the A tile
-  auto tile_coords = [&](int tile, int& bi, int& line, int& pos0) {
+  auto tile_coords = [&](int tile_v, int& bi, int& line, int& pos0) {
+    const int tile = __builtin_amdgcn_readfirstlane(tile_v);  // uniform: keep the division scalar
     const int bl = tile / tpl;
     pos0 = (tile - bl * tpl) * SBM;
     bi = bl / L;
@@ -557,10 +565,17 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
 #pragma unroll
         for (int g4 = 0; g4 < 4; g4++)
           xch[((wc * 2 + mi) * 4 + g4) * 64 + lane] =
-              f32x4{acc[mi][4 * g4], acc[mi][4 * g4 + 1], acc[mi][4 * g4 + 2], acc[mi][4 * g4 + 3]};
+              f32x4{wide_act<EPI>(acc[mi][4 * g4]), wide_act<EPI>(acc[mi][4 * g4 + 1]),
+                    wide_act<EPI>(acc[mi][4 * g4 + 2]), wide_act<EPI>(acc[mi][4 * g4 + 3])};
     }
     __syncthreads();  // the exchange is visible and every wave is done with the A tiles
     if (role == 0) {
+      // all of the exchange first: the staging writes below would otherwise order each read
+      f32x4 sx[2][4];
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) sx[mi][g4] = DUAL ? xch[((wc * 2 + mi) * 4 + g4) * 64 + lane] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mi = 0; mi < 2; mi++)
 #pragma unroll
@@ -568,15 +583,14 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
           const int rq = acc_row32(4 * g4, lane);
           const int cl = CM ? mi * 32 + rq : mi * 32 + (lane & 31);  // first cell (CM: of 4)
           const int ol = CM ? 32 * wc + (lane & 31) : 32 * wc + rq;  // first output (else: of 4)
-          f32x4 d2 = {0.f, 0.f, 0.f, 0.f};
-          if (DUAL) d2 = xch[((wc * 2 + mi) * 4 + g4) * 64 + lane];
+          const f32x4 d2 = sx[mi][g4];
           half4 hv;
 #pragma unroll
           for (int e = 0; e < 4; e++) {
             const int c_e = CM ? cl + e : cl, o_e = CM ? ol : ol + e;
             const bool in = c_e < nvalid && n0 + o_e < p.N;
             const float zv = ZR ? (float)ra.z[ZR ? mi : 0][ZR ? g4 : 0][e] : 0.f;  // zeros past the ends
-            hv[e] = (half_t)wide_value<EPI>(p, acc[mi][4 * g4 + e], d2[e], cell_of(bi, line, pos0 + c_e), in, zv);
+            hv[e] = (half_t)wide_combine<EPI>(p, acc[mi][4 * g4 + e], d2[e], cell_of(bi, line, pos0 + c_e), in, zv);
           }
           if (CM)
             *reinterpret_cast<half4*>(os + ol * OS + cl) = hv;
@@ -608,9 +622,46 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   // this tile's stores, so the stores never hold them up. The A tiles are rewritten only
   // after the barriers that end the previous tile's reads of them, the exchange and the
   // staging area are separate, and the next tile's second barrier orders the staging reuse.
+  // Weights: rows n0 + 32 wc + r of the wave's GEMM (SwiGLU: role 1 holds W1, role 0 W2;
+  // otherwise role 0 W1, role 1 W2). All of the slice's rows are requested at once, the
+  // first tile's loads behind them, then staged through LDS 64 rows at a time so that the
+  // global reads stay row-contiguous.
+  constexpr int WROWS = DUAL ? 2 * BN : BN;     // slice rows: W1's BN, then (DUAL) W2's BN
+  constexpr int WCH = 64 * (K / 8) / WNT;       // 16-byte chunks per thread per 64 rows
+  static_assert(WCH >= 1 && 64 * (K / 8) % WNT == 0, "whole weight chunks per thread");
   const int tg = lg / S;
   Regs r0, r1;
-  gload(r0, tg);
+  {
+    const rsrc_t rW1 = make_rsrc(p.w1), rW2 = make_rsrc(DUAL ? p.w2 : p.w1);
+    half8 wst[WROWS / 64][WCH];
+#pragma unroll
+    for (int r = 0; r < WROWS / 64; r++)
+#pragma unroll
+      for (int q = 0; q < WCH; q++) {
+        const int id = tid + WNT * q, rr = id / (K / 8), j = id - rr * (K / 8);
+        const int g = DUAL ? r * 64 / BN : 0;                // W1 or W2 (64 divides BN; unrolled r)
+        const int n = r * 64 - g * BN + rr;                  // row of that matrix in the slice
+        const uint32_t off = n0 + n < p.N ? (uint32_t)(((size_t)(n0 + n) * K + 8 * j) * 2) : kOOB;
+        wst[r][q] = bload16(g ? rW2 : rW1, off);
+      }
+    gload(r0, tg);
+    constexpr bool SW = EPI == kWideSwiglu;
+    const int my0 = (DUAL ? (SW ? 1 - role : role) * BN : 0) + 32 * wc;  // this wave's first slice row
+#pragma unroll
+    for (int r = 0; r < WROWS / 64; r++) {
+#pragma unroll
+      for (int q = 0; q < WCH; q++) {
+        const int id = tid + WNT * q, rr = id / (K / 8), j = id - rr * (K / 8);
+        st16(a_s + rr * AS + 8 * j, wst[r][q]);
+      }
+      __syncthreads();
+      if (my0 >= r * 64 && my0 < r * 64 + 64) {
+#pragma unroll
+        for (int kk = 0; kk < KW; kk++) wf[kk] = ld16(a_s + (my0 - r * 64 + (lane & 31)) * AS + 16 * kk + 8 * (lane >> 5));
+      }
+      __syncthreads();
+    }
+  }
   gload(r1, tg + stride);
   for (int tile = tg; tile < ntiles; tile += 2 * stride) {
     run_tile(tile, r0);
