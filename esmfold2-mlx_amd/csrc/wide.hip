@@ -24,6 +24,8 @@
 // other LDS buffer. The result is staged in LDS and leaves as whole 16-byte pieces of rows
 // (cell rows for the cell-major outputs, channel rows for GATE_CM). Tiles sharing A rows
 // run on one XCD (their A panel is read once from HBM).
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -194,34 +196,6 @@ DEV float wide_value(const WideArgs& p, float d1, float d2, size_t cell, bool in
 template <int EPI>
 constexpr bool wide_needs_z() { return EPI == kWideResGate || EPI == kWideResid; }
 
-// The weight-stationary kernel splits a dual epilogue between its two GEMMs' waves: the
-// waves of the activated GEMM apply the activation to their own accumulators (wide_act)
-// and pass it through LDS, the other waves finish the output (wide_combine). The operations
-// and their order are those of wide_value, so both kernels give the same bits. For SwiGLU
-// the activated GEMM is the first (silu(d1)), so its waves are the ones that pass.
-template <int EPI>
-DEV float wide_act(float d) {
-  if constexpr (EPI == kWideGateCM) return sigmoidf_fast(d);
-  else if constexpr (EPI == kWideResGate) return sigmoid_from_t(d * kNegLog2e);
-  else return d * sigmoidf_fast(d);  // kWideSwiglu: silu(d1)
-}
-template <int EPI>
-DEV float wide_combine(const WideArgs& p, float d, float s, size_t cell, bool in, float zv) {
-  float v;
-  if constexpr (EPI == kWideGateCM) {
-    v = d * s;
-    if (p.mask) v *= in ? (float)p.mask[cell] : 0.f;
-  } else if constexpr (EPI == kWideResGate) {
-    v = d * s;
-    if (p.mask && p.out_mask) v *= in ? (float)p.mask[cell] : 0.f;
-    if (p.residual) v += zv;
-  } else if constexpr (EPI == kWideSwiglu) {
-    v = s * d;                          // silu(d1) * d2
-  } else {
-    v = wide_value<EPI>(p, d, 0.f, cell, in, zv);
-  }
-  return v;
-}
 
 // Eight waves. DUAL (two GEMMs on the same outputs): a tile is 128 cells x 128 outputs;
 // waves 0-3 compute GEMM 1 and waves 4-7 GEMM 2, each wave 64 cells x 64 outputs (2 x 2
@@ -439,44 +413,67 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
 }
 
 // ---- the weight-stationary wide GEMM (K <= 256) --------------------------------------------
-// Persistent: every workgroup owns a slice of 256 weight rows (DUAL: 128 outputs of W1 and
-// the same 128 of W2; single: 256 outputs of W1), held for the whole launch as MFMA
-// fragments in registers (wave w: 32 rows x K, K / 2 registers), and walks tiles of 64
-// cells of one line; only the A tiles stream, through LDS, the next tile's loads in flight
-// while this one is multiplied. A tile is read by the S workgroups of the S slices, which are
-// neighbours in the XCD-aware order (one L2 fetch). Waves 0-3 of a DUAL slice take GEMM 1
-// and 4-7 GEMM 2 for the same outputs; GEMM 2's sums reach GEMM 1's waves through LDS at the
-// same (block, register, lane). Same arithmetic, same order of the K sums, same bits as
-// wide_gemm_kernel.
+// Persistent: every workgroup owns a slice of the outputs (DUAL: 128 outputs of W1 and the
+// same 128 of W2; single: 256 outputs of W1) and holds the slice's weight rows for the whole
+// launch as v_mfma_f32_16x16x32_f16 fragments in registers: wave w takes 16 outputs of both
+// GEMMs (DUAL) or 32 outputs (single), K / 4 registers either way. Tiles of 64 cells of one
+// line stream through LDS with two tiles' loads in flight. A wave holds both GEMMs' sums for
+// the same (cell, output) positions, so it finishes its outputs by itself: no exchange
+// between waves, two barriers per tile, and one wave's epilogue runs under the other wave's
+// MFMAs on the same SIMD. A tile is read by the S workgroups of the S slices, which are
+// neighbours in the XCD-aware order (one L2 fetch).
 namespace {
 constexpr int SBM = 64;   // cells per tile
 }  // namespace
 
+// The epilogue of wide_value with the mask (HM) and the residual (RS) fixed per launch.
+template <int EPI, bool HM, bool RS>
+DEV float wide_value_u(const WideArgs& p, float d1, float d2, size_t cell, bool in, float zv) {
+  float v;
+  if constexpr (EPI == kWideGateCM) {
+    v = d1 * sigmoidf_fast(d2);
+    if constexpr (HM) v *= in ? (float)p.mask[cell] : 0.f;
+  } else if constexpr (EPI == kWideResGate) {
+    v = d1 * sigmoid_from_t(d2 * kNegLog2e);
+    if constexpr (HM) v *= in ? (float)p.mask[cell] : 0.f;
+    if constexpr (RS) v += zv;
+  } else if constexpr (EPI == kWideRelu) {
+    v = fmaxf(d1, 0.f);
+  } else if constexpr (EPI == kWideSwiglu) {
+    v = d1 * sigmoidf_fast(d1) * d2;
+  } else {  // kWideResid
+    v = d1 + zv;
+  }
+  return v;
+}
+
 template <int EPI, bool DUAL, bool A2SEP, int KW>  // KW = K / 16
 __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   constexpr int K = 16 * KW;
+  constexpr int KS = K / 32;                    // k-steps of the 16x16x32 MFMA
   constexpr int NA = A2SEP ? 2 : 1;
   constexpr int BN = DUAL ? 128 : 256;          // outputs per slice
+  constexpr int NOB = DUAL ? 1 : 2;             // 16-output blocks per wave
   constexpr int AS = K + 8;                     // LDS row stride (halfs) of an A tile
   constexpr int A_HALFS = NA * SBM * AS;
   constexpr bool CM = EPI == kWideGateCM;
+  constexpr bool ZR = wide_needs_z<EPI>();      // the residual comes in with the A tile
   constexpr int OS = CM ? SBM + 8 : BN + 8;     // staging row stride: [o][cell] or [cell][o]
   constexpr int OUT_HALFS = CM ? BN * OS : SBM * OS;
-  constexpr int XCH_BYTES = DUAL ? 4 * 2 * 4 * 64 * 16 : 0;
   constexpr int WST_HALFS = 64 * AS;            // start-up: 64 weight rows at a time
-  constexpr int MAIN_BYTES = A_HALFS * 2 + XCH_BYTES + OUT_HALFS * 2;
+  constexpr int MAIN_BYTES = A_HALFS * 2 + OUT_HALFS * 2;
   constexpr int SMEM_BYTES = MAIN_BYTES > WST_HALFS * 2 ? MAIN_BYTES : WST_HALFS * 2;
   constexpr int CH_A = SBM * (K / 8) / WNT;     // 16-byte loads per thread per A tile
   static_assert(CH_A >= 1 && SBM * (K / 8) % WNT == 0, "whole loads per thread");
+  static_assert(KS >= 1 && K % 32 == 0, "K a multiple of 32");
+  static_assert(!(CM && ZR), "no residual with channel-major planes");
   __shared__ __align__(16) char smem_c[SMEM_BYTES];
   half_t* a_s = reinterpret_cast<half_t*>(smem_c);
-  f32x4* xch = reinterpret_cast<f32x4*>(smem_c + A_HALFS * 2);
-  half_t* os = reinterpret_cast<half_t*>(smem_c + A_HALFS * 2 + XCH_BYTES);
+  half_t* os = reinterpret_cast<half_t*>(smem_c + A_HALFS * 2);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int role = DUAL ? wave >> 2 : 0;
-  const int wc = DUAL ? wave & 3 : wave;        // 32-output block of this wave
+  const int l16 = lane & 15, q4 = lane >> 4;
   const int L = p.L;
   const int S = (p.N + BN - 1) / BN;            // slices
   const int lg = xcd_remap(blockIdx.x, gridDim.x);
@@ -485,11 +482,15 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   const int stride = gridDim.x / S;             // tile groups
   const int tpl = (L + SBM - 1) / SBM;
   const int ntiles = p.B * L * tpl;
+  // first output (in the slice) of 16-output block b of this wave
+  const int ob0 = DUAL ? 16 * wave : 32 * wave;
 
-  half8 wf[KW];  // this wave's 32 weight rows as MFMA fragments, for the whole launch
+  // fragment set f: DUAL: W1 (f = 0), W2 (f = 1) for outputs ob0 .. ob0+15;
+  // single: W1 for outputs ob0 + 16 f .. +15. Lane: row l16 of the set, k = 32 ks + 8 q4 + e.
+  half8 wf[2][KS];
+
   const rsrc_t rA1 = make_rsrc(p.a1), rA2 = make_rsrc(A2SEP ? p.a2 : p.a1);
-  const rsrc_t rZ = make_rsrc(wide_needs_z<EPI>() ? (const void*)p.z : (const void*)p.a1);
-  constexpr bool ZR = wide_needs_z<EPI>();      // the residual comes in with the A tile
+  const rsrc_t rZ = make_rsrc(ZR ? (const void*)p.z : (const void*)p.a1);
   auto tile_coords = [&](int tile_v, int& bi, int& line, int& pos0) {
     const int tile = __builtin_amdgcn_readfirstlane(tile_v);  // uniform: keep the division scalar
     const int bl = tile / tpl;
@@ -502,10 +503,10 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   };
   struct Regs {
     half8 a[NA][CH_A];
-    half4 z[ZR ? 2 : 1][ZR ? 4 : 1];            // role 0: z[cell][4 outputs] per (mi, group)
+    half4 z[ZR ? NOB : 1][ZR ? 4 : 1];          // z[cell 16 cb + l16][outputs ob + 4 q4 .. +3]
   };
-  // One tile's loads: the A rows (every thread), and for the GEMM-1 waves the residual pieces
-  // they add: lane (cell mi*32 + lane%32, outputs 32 wc + acc_row32(4 g4) .. +3), 8 bytes each.
+  // One tile's loads: the A rows (row-contiguous 16-byte pieces), and the residual pieces
+  // this lane adds, 8 bytes each.
   auto gload = [&](Regs& r, int tile) {
     const bool live = tile < ntiles;
     int bi, line, pos0;
@@ -519,20 +520,20 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
       if constexpr (A2SEP) r.a[1][u] = bload16(rA2, off);
     }
     if constexpr (ZR) {
-      const bool want = role == 0 && (EPI == kWideResid || p.residual);
+      const bool want = EPI == kWideResid || p.residual;
 #pragma unroll
-      for (int mi = 0; mi < 2; mi++)
+      for (int b = 0; b < NOB; b++)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-          const int c = mi * 32 + (lane & 31), o = n0 + 32 * wc + acc_row32(4 * g4, lane);
+        for (int cb = 0; cb < 4; cb++) {
+          const int c = 16 * cb + l16, o = n0 + ob0 + 16 * b + 4 * q4;
           const bool ok = want && live && pos0 + c < L && o < p.N;
           const uint32_t off = ok ? (uint32_t)(cell_of(bi, line, pos0 + c) * p.ldo + o) * 2u : kOOB;
-          r.z[mi][g4] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(rZ, (int)off, 0, 0));
+          r.z[b][cb] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(rZ, (int)off, 0, 0));
         }
     }
   };
 
-  // one tile: A tiles to LDS, the MFMAs, the exchange, the epilogue, the stores
+  // one tile: A tiles to LDS, the MFMAs, each wave's own epilogue into the staging tile, stores
   auto run_tile = [&](int tile, const Regs& ra) {
     int bi, line, pos0;
     tile_coords(tile, bi, line, pos0);
@@ -544,61 +545,58 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
         const int id = tid + WNT * u, row = id / (K / 8), j = id - row * (K / 8);
         st16(a_s + (pa * SBM + row) * AS + 8 * j, ra.a[pa][u]);
       }
-    __syncthreads();
-    // D over this wave's 32 outputs and the tile's 64 cells: 2 chains of KW MFMAs
-    f32x16 acc[2];
+    __syncthreads();  // the A tiles are in LDS; the previous tile's staging reads are done
+    f32x4 acc[2][4];
 #pragma unroll
-    for (int mi = 0; mi < 2; mi++)
+    for (int f = 0; f < 2; f++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) acc[mi][e] = 0.f;
-    const half_t* at = a_s + (A2SEP ? role * SBM : 0) * AS;
+      for (int cb = 0; cb < 4; cb++) acc[f][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < KW; kk++)
+    for (int ks = 0; ks < KS; ks++)
 #pragma unroll
-      for (int mi = 0; mi < 2; mi++) {
-        const half8 af = ld16(at + (mi * 32 + (lane & 31)) * AS + 16 * kk + 8 * (lane >> 5));
-        acc[mi] = CM ? mfma32(af, wf[kk], acc[mi]) : mfma32(wf[kk], af, acc[mi]);
+      for (int cb = 0; cb < 4; cb++) {
+        const half8 a1 = ld16(a_s + (16 * cb + l16) * AS + 32 * ks + 8 * q4);
+        const half8 a2 = A2SEP ? ld16(a_s + (SBM + 16 * cb + l16) * AS + 32 * ks + 8 * q4) : a1;
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+          const half8 af = (A2SEP && f == 1) ? a2 : a1;
+          // CM: D[cell][output] (a lane ends with 4 consecutive cells of one output);
+          // otherwise D[output][cell] (4 consecutive outputs of one cell)
+          acc[f][cb] = CM ? mfma16(af, wf[f][ks], acc[f][cb]) : mfma16(wf[f][ks], af, acc[f][cb]);
+        }
       }
-    if (DUAL && role == 1) {
+    auto finish = [&](auto hm, auto rs) {
+      constexpr bool HM = decltype(hm)::value, RS = decltype(rs)::value;
 #pragma unroll
-      for (int mi = 0; mi < 2; mi++)
+      for (int b = 0; b < NOB; b++)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; g4++)
-          xch[((wc * 2 + mi) * 4 + g4) * 64 + lane] =
-              f32x4{wide_act<EPI>(acc[mi][4 * g4]), wide_act<EPI>(acc[mi][4 * g4 + 1]),
-                    wide_act<EPI>(acc[mi][4 * g4 + 2]), wide_act<EPI>(acc[mi][4 * g4 + 3])};
-    }
-    __syncthreads();  // the exchange is visible and every wave is done with the A tiles
-    if (role == 0) {
-      // all of the exchange first: the staging writes below would otherwise order each read
-      f32x4 sx[2][4];
-#pragma unroll
-      for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) sx[mi][g4] = DUAL ? xch[((wc * 2 + mi) * 4 + g4) * 64 + lane] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-          const int rq = acc_row32(4 * g4, lane);
-          const int cl = CM ? mi * 32 + rq : mi * 32 + (lane & 31);  // first cell (CM: of 4)
-          const int ol = CM ? 32 * wc + (lane & 31) : 32 * wc + rq;  // first output (else: of 4)
-          const f32x4 d2 = sx[mi][g4];
+        for (int cb = 0; cb < 4; cb++) {
           half4 hv;
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            const int c_e = CM ? cl + e : cl, o_e = CM ? ol : ol + e;
-            const bool in = c_e < nvalid && n0 + o_e < p.N;
-            const float zv = ZR ? (float)ra.z[ZR ? mi : 0][ZR ? g4 : 0][e] : 0.f;  // zeros past the ends
-            hv[e] = (half_t)wide_combine<EPI>(p, acc[mi][4 * g4 + e], d2[e], cell_of(bi, line, pos0 + c_e), in, zv);
+            const int cl = CM ? 16 * cb + 4 * q4 + e : 16 * cb + l16;
+            const int ol = CM ? ob0 + l16 : ob0 + 16 * b + 4 * q4 + e;
+            const bool in = cl < nvalid && n0 + ol < p.N;
+            const float d1 = acc[DUAL ? 0 : b][cb][e], d2 = DUAL ? acc[1][cb][e] : 0.f;
+            const float zv = ZR ? (float)ra.z[ZR ? b : 0][ZR ? cb : 0][e] : 0.f;  // zeros past the ends
+            hv[e] = (half_t)wide_value_u<EPI, HM, RS>(p, d1, d2, HM ? cell_of(bi, line, pos0 + cl) : 0, in, zv);
           }
           if (CM)
-            *reinterpret_cast<half4*>(os + ol * OS + cl) = hv;
+            *reinterpret_cast<half4*>(os + (ob0 + l16) * OS + 16 * cb + 4 * q4) = hv;
           else
-            *reinterpret_cast<half4*>(os + cl * OS + ol) = hv;
+            *reinterpret_cast<half4*>(os + (16 * cb + l16) * OS + ob0 + 16 * b + 4 * q4) = hv;
         }
+    };
+    const bool hm = (EPI == kWideGateCM && p.mask) || (EPI == kWideResGate && p.mask && p.out_mask);
+    const bool rs = EPI == kWideResid || (EPI == kWideResGate && p.residual);
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    if (hm) {
+      if (rs) finish(T_{}, T_{}); else finish(T_{}, F_{});
+    } else {
+      if (rs) finish(F_{}, T_{}); else finish(F_{}, F_{});
     }
-    __syncthreads();  // the staged tile is complete
+    __syncthreads();  // the staged tile is complete; every wave is done with the A tiles
     if constexpr (CM) {
       for (int id = tid; id < BN * (SBM / 8); id += WNT) {
         const int o = id / (SBM / 8), q = id - o * (SBM / 8);
@@ -617,16 +615,11 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
     }
   };
 
-  // Two tiles' loads in flight: a tile's registers are reloaded (two tiles ahead) only after
-  // its epilogue has used them. Tiles of the next iteration wait for loads issued before
-  // this tile's stores, so the stores never hold them up. The A tiles are rewritten only
-  // after the barriers that end the previous tile's reads of them, the exchange and the
-  // staging area are separate, and the next tile's second barrier orders the staging reuse.
-  // Weights: rows n0 + 32 wc + r of the wave's GEMM (SwiGLU: role 1 holds W1, role 0 W2;
-  // otherwise role 0 W1, role 1 W2). All of the slice's rows are requested at once, the
-  // first tile's loads behind them, then staged through LDS 64 rows at a time so that the
-  // global reads stay row-contiguous.
-  constexpr int WROWS = DUAL ? 2 * BN : BN;     // slice rows: W1's BN, then (DUAL) W2's BN
+  // Weights: the slice's rows (DUAL: W1's BN, then W2's BN) are requested at once, the first
+  // tile's loads behind them, then staged through LDS 64 rows at a time so that the global
+  // reads stay row-contiguous (fragment-pattern reads straight from global memory were no
+  // faster: the start-up is bound by the 128 KB each workgroup pulls through its L1).
+  constexpr int WROWS = DUAL ? 2 * BN : BN;
   constexpr int WCH = 64 * (K / 8) / WNT;       // 16-byte chunks per thread per 64 rows
   static_assert(WCH >= 1 && 64 * (K / 8) % WNT == 0, "whole weight chunks per thread");
   const int tg = lg / S;
@@ -645,8 +638,6 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
         wst[r][q] = bload16(g ? rW2 : rW1, off);
       }
     gload(r0, tg);
-    constexpr bool SW = EPI == kWideSwiglu;
-    const int my0 = (DUAL ? (SW ? 1 - role : role) * BN : 0) + 32 * wc;  // this wave's first slice row
 #pragma unroll
     for (int r = 0; r < WROWS / 64; r++) {
 #pragma unroll
@@ -655,14 +646,24 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
         st16(a_s + rr * AS + 8 * j, wst[r][q]);
       }
       __syncthreads();
-      if (my0 >= r * 64 && my0 < r * 64 + 64) {
 #pragma unroll
-        for (int kk = 0; kk < KW; kk++) wf[kk] = ld16(a_s + (my0 - r * 64 + (lane & 31)) * AS + 16 * kk + 8 * (lane >> 5));
+      for (int f = 0; f < 2; f++) {
+        const int sb = DUAL ? f * BN + ob0 : ob0 + 16 * f;  // the set's first slice row
+        if (sb >= r * 64 && sb < r * 64 + 64) {
+#pragma unroll
+          for (int ks = 0; ks < KS; ks++) wf[f][ks] = ld16(a_s + (sb - r * 64 + l16) * AS + 32 * ks + 8 * q4);
+        }
       }
       __syncthreads();
     }
   }
   gload(r1, tg + stride);
+
+  // Two tiles' loads in flight: a tile's registers are reloaded (two tiles ahead) only after
+  // its epilogue has used them; the next tile's loads were issued before this tile's stores,
+  // so waiting for them never waits for the stores. The A tiles are rewritten only after the
+  // second barrier of the previous tile (every wave's MFMAs done), and the staging tile only
+  // after the first barrier of the next tile (every thread's stores read).
   for (int tile = tg; tile < ntiles; tile += 2 * stride) {
     run_tile(tile, r0);
     gload(r0, tile + 2 * stride);
