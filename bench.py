@@ -369,6 +369,24 @@ def main():
             by = Nd * Kd + 2 * 2 * Nd * (Kd // 64) + 2 * L * Kd + 2 * L * Nd
             qres[name] = {"us": t * 1e6, "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
                           "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK, "split_k": ws is not None}
+        # the quantiser (layer_params' mx.quantize) on the largest ESMC weight, w1 [10240, 2560] fp32:
+        # reads 4 B per weight, writes a code per weight and an fp16 scale and bias per 64
+        Nw, Kw = 10240, 2560
+        wf = torch.randn(Nw, Kw, generator=torch.Generator().manual_seed(11)).mul_(0.02).to(dev)
+        for _ in range(3):
+            K.q8_quantize(wf)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        reps = 20
+        for _ in range(reps):
+            K.q8_quantize(wf)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        by = 5 * Nw * Kw + 4 * Nw * (Kw // 64)
+        qres[f"quantize {Nw}x{Kw}"] = {"us": t * 1e6, "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK}
+        del wf
         out["q8"] = qres
 
     stack_case = None
