@@ -104,16 +104,24 @@ const char* esm_source_hash(void) { return kSourceTag + 7; }
 
 int tmu_leading_dim(int L) { return L <= 0 ? 0 : round_up(L, 8); }
 
+// Halfs per channel of one workspace plane: the larger of [L, ld] and the fragment layout
+// the fused forward's operands use.
+static size_t tmu_plane_halfs(int L) {
+  const size_t rows = (size_t)L * tmu_leading_dim(L), frag = esm::FragLayout::plane_halfs(L);
+  return rows > frag ? rows : frag;
+}
+
 size_t tmu_workspace_bytes(int B, int L, int c) {
   if (B <= 0 || L <= 0 || c <= 0) return 0;
-  const size_t plane = (size_t)B * c * L * tmu_leading_dim(L) * sizeof(esm_half);
+  const size_t plane = (size_t)B * c * tmu_plane_halfs(L) * sizeof(esm_half);
   const size_t a256 = (plane + 255) / 256 * 256;
   return (c == 128 ? 3 : 4) * a256;  // a, b, x (and the wide path's LN_in(z) plane)
 }
 
-int tmu_project(const esm_half* z, const esm_half* mask, const float* ln_w, const float* ln_b, float ln_eps,
-                const esm_half* w, esm_half* a_out, esm_half* b_out, int B, int L, int C, int c, int ld,
-                int incoming, void* stream) {
+// frag: write a, b in the fragment layout (the fused forward) instead of [B, c, L, ld].
+static int project_impl(const esm_half* z, const esm_half* mask, const float* ln_w, const float* ln_b, float ln_eps,
+                        const esm_half* w, esm_half* a_out, esm_half* b_out, int B, int L, int C, int c, int ld,
+                        int incoming, bool frag, void* stream) {
   if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_project: B=%d L=%d must be >= 0", B, L);
   if (C != 128 || c != 128) return fail(ESM_ERR_UNSUPPORTED, "tmu_project: C=%d c=%d (supported: 128, 128)", C, c);
   if (B == 0 || L == 0) return ok();
@@ -127,12 +135,27 @@ int tmu_project(const esm_half* z, const esm_half* mask, const float* ln_w, cons
   if (!(ln_eps >= 0.f)) return fail(ESM_ERR_SHAPE, "tmu_project: eps must be >= 0");
   esm::ProjectArgs a{H(z), mask ? H(mask) : nullptr, ln_w, ln_b, ln_eps, H(w), H(a_out), H(b_out), B, L, ld,
                      incoming ? 1 : 0, 0, 0};
-  a.tiles_per_line = (L + esm::kCellTile - 1) / esm::kCellTile;
-  const long long ntiles = (long long)B * L * a.tiles_per_line;
+  long long ntiles;
+  if (frag) {  // blocks of 8 x 8 cells
+    a.frag = 1;
+    a.rbn = (L + 31) / 32;
+    a.kbn = (L + 15) / 16;
+    a.tiles_per_line = (L + 7) / 8;
+    ntiles = (long long)B * a.tiles_per_line * a.tiles_per_line;
+  } else {
+    a.tiles_per_line = (L + esm::kCellTile - 1) / esm::kCellTile;
+    ntiles = (long long)B * L * a.tiles_per_line;
+  }
   if (ntiles > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_project: too many tiles");
   a.ntiles = (int)ntiles;
   const int grid = (int)(ntiles < cu_count() ? ntiles : cu_count());
   return hip_status(esm::launch_project(a, grid, (hipStream_t)stream), "tmu_project launch");
+}
+
+int tmu_project(const esm_half* z, const esm_half* mask, const float* ln_w, const float* ln_b, float ln_eps,
+                const esm_half* w, esm_half* a_out, esm_half* b_out, int B, int L, int C, int c, int ld,
+                int incoming, void* stream) {
+  return project_impl(z, mask, ln_w, ln_b, ln_eps, w, a_out, b_out, B, L, C, c, ld, incoming, false, stream);
 }
 
 int tmu_contract(const esm_half* a, const esm_half* b, esm_half* x, int batch, int L, int ld, int ldx, float scale,
@@ -278,7 +301,7 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
     return fail(ESM_ERR_ALIGN, "tmu_forward: workspace must be 256-byte aligned");
   const int ld = tmu_leading_dim(L);
-  const size_t plane = (size_t)B * c * L * ld;
+  const size_t plane = (size_t)B * c * tmu_plane_halfs(L);
   const size_t a256 = (plane * sizeof(esm_half) + 255) / 256 * 256 / sizeof(esm_half);
   esm_half* wa = static_cast<esm_half*>(workspace);
   esm_half* wb = wa + a256;
@@ -286,10 +309,14 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
   // fp16 range scheme (mlx_trunk.py:14-19): the contraction is stored as x/256
   // and norm_mix's eps divided by 256^2; LN(x/s, eps/s^2) == LN(x, eps) exactly.
   const float kScale = 1.0f / 256.0f;
-  int rc = tmu_project(z, mask, ln_in_w, ln_in_b, ln_in_eps, w_bundle, wa, wb, B, L, C, c, ld, outgoing ? 0 : 1,
-                       stream);
+  // a and b go through the workspace in the fragment layout: the contraction then loads
+  // every operand fragment straight into registers (same bits as the [B, c, L, ld] path)
+  int rc = project_impl(z, mask, ln_in_w, ln_in_b, ln_in_eps, w_bundle, wa, wb, B, L, C, c, ld, outgoing ? 0 : 1,
+                        true, stream);
   if (rc) return rc;
-  rc = tmu_contract(wa, wb, wx, B * c, L, ld, ld, kScale, stream);
+  if (B * c > 65535) return fail(ESM_ERR_SHAPE, "tmu_forward: B=%d too large", B);
+  esm::ContractArgs ca{H(wa), H(wb), H(wx), B * c, L, ld, ld, kScale, 1};
+  rc = hip_status(esm::launch_contract(ca, (hipStream_t)stream), "tmu_forward contract launch");
   if (rc) return rc;
   return tmu_epilogue(wx, ld, z, mask, ln_in_w, ln_in_b, ln_in_eps, ln_mix_w, ln_mix_b, ln_mix_eps * kScale * kScale,
                       w_emit, w_gate, out, B, L, C, c, residual, out_mask, stream);

@@ -163,7 +163,104 @@ __global__ __launch_bounds__(NT, 2) void tmu_contract_kernel(ContractArgs p) {
   }
 }
 
+// The same contraction on operands in FragLayout (written so by kernel (a) in the fused
+// forward): every MFMA fragment is one fully coalesced 1 KB load straight into registers,
+// so there is no LDS staging and no barrier in the K loop. A workgroup computes a 128 x 128
+// block as 2 x 2 waves of 64 x 64 (the two waves that share A rows, or B rows, read them
+// within a few cycles of each other: one L2 fetch); each wave keeps NSF k-steps of
+// fragments in flight. Lanes whose row is at or past L, or whose 8 k start at or past L,
+// load zeros (rows past L are never written; k past L is zero up to the 8-aligned edge).
+// Same MFMAs in the same order as tmu_contract_kernel: the same bits. The output tile is
+// staged per wave in LDS and leaves as whole 128-byte row segments.
+namespace {
+constexpr int NSF = 3;             // k-steps in flight per wave
+constexpr int FSR = 64 + 8;        // per-wave staging row stride (halfs)
+}  // namespace
+
+__global__ __launch_bounds__(256, 2) void tmu_contract_frag_kernel(ContractArgs p) {
+  __shared__ __align__(16) half_t stg[4][64 * FSR];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 1, wc = wave & 1;
+  const int L = p.L;
+  const int rbn = (L + 31) / 32, kbn = (L + 15) / 16;
+  const int nb = (rbn + 3) / 4;                    // 128-row blocks per dimension
+  const int t = xcd_remap(blockIdx.x, gridDim.x);  // a channel's nb^2 blocks share an L2
+  const int ch = t / (nb * nb), rem = t - ch * nb * nb;
+  const int bi = rem / nb, bj = rem - bi * nb;
+  const int rb0 = (bi * 2 + wr) * 2, cb0 = (bj * 2 + wc) * 2;  // first 32-row block of A and of B
+  const size_t plane = (size_t)rbn * kbn * FragLayout::kTileHalfs;
+  const rsrc_t rA = make_rsrc(p.a + (size_t)ch * plane), rB = make_rsrc(p.b + (size_t)ch * plane);
+  const int lr = lane & 31, lk = 8 * (lane >> 5);
+  auto toff = [&](int rb, int kb) -> uint32_t {
+    const bool ok = rb < rbn && 32 * rb + lr < L && kb < kbn && 16 * kb + lk < L;
+    return ok ? (uint32_t)((((size_t)rb * kbn + kb) * 64 + lane) * 16) : kOOB;
+  };
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int v = 0; v < 2; v++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[u][v][e] = 0.f;
+  half8 fa[NSF][2], fb[NSF][2];
+#pragma unroll
+  for (int st = 0; st < NSF; st++)
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      fa[st][u] = bload16(rA, toff(rb0 + u, st));
+      fb[st][u] = bload16(rB, toff(cb0 + u, st));
+    }
+  // k-steps past kbn load zeros and add nothing; the loop runs a whole number of rounds
+  const int nk = (kbn + NSF - 1) / NSF * NSF;
+  for (int k0 = 0; k0 < nk; k0 += NSF) {
+#pragma unroll
+    for (int st = 0; st < NSF; st++) {
+#pragma unroll
+      for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int v = 0; v < 2; v++) acc[u][v] = mfma32(fb[st][v], fa[st][u], acc[u][v]);  // D[j][i]
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        fa[st][u] = bload16(rA, toff(rb0 + u, k0 + NSF + st));
+        fb[st][u] = bload16(rB, toff(cb0 + u, k0 + NSF + st));
+      }
+    }
+  }
+  // lane: i = 32u + lane % 32, j = 32v + 8g + 4 (lane / 32) .. +3
+  half_t* sw = stg[wave];
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int v = 0; v < 2; v++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        half4 h;
+#pragma unroll
+        for (int e = 0; e < 4; e++) h[e] = (half_t)(acc[u][v][4 * g + e] * p.scale);
+        *reinterpret_cast<half4*>(sw + (32 * u + lr) * FSR + acc_row32(4 * g, lane) + 32 * v) = h;
+      }
+  // the staging rows are private to the wave; this keeps the reads below the writes
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int i0 = 32 * rb0, j0 = 32 * cb0;
+  const rsrc_t rX = make_rsrc(p.x + ((size_t)ch * L) * p.ldx);
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    const int row = 8 * q + (lane >> 3), chunk = lane & 7;
+    const int i = i0 + row, j = j0 + 8 * chunk;
+    const bool ok = i < L && j < p.ldx;
+    bstore16(rX, ok ? (uint32_t)((size_t)i * p.ldx + j) * 2u : kOOB, ld16(sw + row * FSR + 8 * chunk));
+  }
+}
+
 hipError_t launch_contract(const ContractArgs& a, hipStream_t s) {
+  if (a.frag) {
+    const int nb = ((a.L + 31) / 32 + 3) / 4;
+    hipLaunchKernelGGL(tmu_contract_frag_kernel, dim3((unsigned)((long long)a.batch * nb * nb)), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   const long long blocks = (long long)a.batch * ((a.L + BM - 1) / BM) * ((a.L + BN - 1) / BN);
   hipLaunchKernelGGL(tmu_contract_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
   return hipGetLastError();

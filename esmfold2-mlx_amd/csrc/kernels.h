@@ -21,14 +21,29 @@ struct ProjectArgs {
   int B, L, ld;
   int transpose;        // 1: store cell (r, s) at row s, column r
   int ntiles, tiles_per_line;
+  // frag = 1: a and b in MFMA-fragment order instead of [B, c, L, ld] (see FragLayout),
+  // with tiles of 8 x 8 cells (tiles_per_line = tiles per dimension)
+  int frag, rbn, kbn;
+};
+
+// The MFMA-fragment layout of a contraction operand (kernel (a) writes it for the fused
+// forward, kernel (b) reads it): plane p = b * c + channel holds rbn x kbn tiles of 32 rows
+// by 16 k, rbn = ceil(L / 32), kbn = ceil(L / 16); a tile is 64 lanes x 8 halfs, lane l
+// holding row 32 rb + l % 32, k = 16 kb + 8 (l / 32) .. +7, i.e. exactly the operand of one
+// v_mfma_f32_32x32x16_f16, so the contraction loads each operand fragment with one fully
+// coalesced 1 KB read. Rows at or past L are never read; k at or past L is zero.
+struct FragLayout {
+  static constexpr int kTileHalfs = 64 * 8;
+  static size_t plane_halfs(int L) { return (size_t)((L + 31) / 32) * ((L + 15) / 16) * kTileHalfs; }
 };
 
 struct ContractArgs {
-  const half_t* a;      // [batch, L, ld]
-  const half_t* b;      // [batch, L, ld]
+  const half_t* a;      // [batch, L, ld], or (frag) [batch] planes of FragLayout
+  const half_t* b;      // [batch, L, ld], or (frag) [batch] planes of FragLayout
   half_t* x;            // [batch, L, ldx]
   int batch, L, ld, ldx;
   float scale;
+  int frag;             // operands in FragLayout
 };
 
 struct EpilogueArgs {

@@ -50,7 +50,7 @@ DEV int st_off(int ch, int cell) {  // in halfs
   return ch * TM + 8 * ((cell >> 3) ^ ((ch >> 1) & 7)) + (cell & 7);
 }
 
-template <bool HAS_MASK>
+template <bool HAS_MASK, bool FRAG>
 __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) {
   __shared__ __align__(16) half_t n_s[2][TM * NS];
   __shared__ __align__(16) float m_s[2][TM];
@@ -93,14 +93,38 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
     bb[e] = p.ln_b[ch0 + e];
   }
 
-  // Tile coordinates: `line` is the fixed grid index, positions pos0 .. pos0+63 vary.
+  // Tile coordinates. Row-major planes: `line` is the fixed grid index, positions
+  // pos0 .. pos0+63 vary. FRAG: a block of 8 x 8 cells, operand rows line .. line+7 and
+  // k pos0 .. pos0+7 (tile cell cl = 8 dr + dc is row line + dr, k pos0 + dc).
   auto coords = [&](int tile, int& bi, int& line, int& pos0) {
-    const int bl = tile / p.tiles_per_line;
-    pos0 = (tile - bl * p.tiles_per_line) * TM;
-    bi = bl / L;
-    line = bl - bi * L;
+    if constexpr (FRAG) {
+      const int per = p.tiles_per_line * p.tiles_per_line;
+      bi = tile / per;
+      const int t = tile - bi * per;
+      const int tr = t / p.tiles_per_line;
+      line = 8 * tr;
+      pos0 = 8 * (t - tr * p.tiles_per_line);
+    } else {
+      const int bl = tile / p.tiles_per_line;
+      pos0 = (tile - bl * p.tiles_per_line) * TM;
+      bi = bl / L;
+      line = bl - bi * L;
+    }
   };
   const uint32_t cstride = p.transpose ? (uint32_t)L : 1u;  // cell stride along the tile
+  // Offset (in cells, from the tile's first cell) of tile cell cl, and whether it is in range.
+  auto cell_off = [&](int cl) -> uint32_t {
+    if constexpr (FRAG) {
+      const uint32_t dr = cl >> 3, dc = cl & 7;   // operand row line + dr, k pos0 + dc
+      return p.transpose ? dc * (uint32_t)L + dr : dr * (uint32_t)L + dc;
+    } else {
+      return cl * cstride;
+    }
+  };
+  auto cell_ok = [&](int line, int pos0, int cl) -> bool {
+    if constexpr (FRAG) return line + (cl >> 3) < L && pos0 + (cl & 7) < L;
+    else return pos0 + cl < L;
+  };
 
   // Issue one tile's loads: z (16 lanes per cell, 8 channels per lane) and the raw mask.
   // A tile index past the end (the pipeline's last prefetch) loads nothing.
@@ -109,15 +133,17 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
     int bi, line, pos0;
     coords(live ? tile : 0, bi, line, pos0);
     const size_t cb = (size_t)bi * L * L + (p.transpose ? (size_t)pos0 * L + line : (size_t)line * L + pos0);
+    // (FRAG: the tile's first cell is operand row `line`, k `pos0`: cell (line, pos0), or
+    // (pos0, line) transposed, the same formula)
     const rsrc_t rz = make_rsrc(p.z + cb * C);
     const rsrc_t rm = make_rsrc(has_mask ? (const void*)(p.mask + cb) : (const void*)p.z);
     (void)rm;
 #pragma unroll
     for (int it = 0; it < CPT; it++) {
       const int cl = (tid >> 4) + (NW * 4) * it;
-      const bool ok = live && pos0 + cl < L;
-      zq[it] = bload16(rz, ok ? (uint32_t)(cl * cstride * C + ch0) * 2u : kOOB);
-      if (has_mask) mq[it] = bload2(rm, ok ? (uint32_t)(cl * cstride) * 2u : kOOB);
+      const bool ok = live && cell_ok(line, pos0, cl);
+      zq[it] = bload16(rz, ok ? (uint32_t)(cell_off(cl) * C + ch0) * 2u : kOOB);
+      if (has_mask) mq[it] = bload2(rm, ok ? cell_off(cl) * 2u : kOOB);
     }
   };
 
@@ -138,7 +164,7 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
       // Cells past L (zeros from the range-checked loads) enter the projection as zeros,
       // so their padded outputs [L, ld) are exactly 0 with or without a mask (their
       // LayerNorm would be 0 * rsqrt(eps), NaN for eps = 0).
-      const bool cell_in = pos0 + cl < L;
+      const bool cell_in = cell_ok(line, pos0, cl);
       half8 o;
 #pragma unroll
       for (int e = 0; e < 8; e++) o[e] = cell_in ? (half_t)v[e] : (half_t)0.f;
@@ -190,16 +216,30 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // 3. Whole 128-byte row segments: 8 lanes x 16 B per channel row, 8 rows per store.
-    //    Chunks at or past ld are dropped by the buffer range check.
-    const size_t row0 = ((size_t)bi * CL + ch_base) * L + line;  // this wave's first channel row
-    const rsrc_t ro = make_rsrc((is_b ? p.b : p.a) + row0 * p.ld + pos0);
+    //    Chunks at or past ld are dropped by the buffer range check. FRAG: the staged row
+    //    of a channel (8 operand rows x 8 k) is lanes 32 (pos0 / 8 % 2) + line % 32 .. +7
+    //    of one fragment tile: again one whole 128-byte segment.
     const int q = lane & 7;
-    const bool okq = pos0 + q * 8 < p.ld;
+    if constexpr (FRAG) {
+      const size_t tile_h = ((size_t)(line >> 5) * p.kbn + (pos0 >> 4)) * FragLayout::kTileHalfs +
+                            (size_t)((line & 31) + 32 * ((pos0 >> 3) & 1)) * 8;
+      const size_t plane_h = (size_t)p.rbn * p.kbn * FragLayout::kTileHalfs;
+      const rsrc_t ro = make_rsrc((is_b ? p.b : p.a) + ((size_t)bi * CL + ch_base) * plane_h + tile_h);
 #pragma unroll
-    for (int u = 0; u < CPW / 8; u++) {
-      const int ch = 8 * u + (lane >> 3);
-      const uint32_t off = okq ? (uint32_t)((size_t)ch * L * p.ld + q * 8) * 2u : kOOB;
-      bstore16(ro, off, ld16(&st[st_off(ch, q * 8)]));
+      for (int u = 0; u < CPW / 8; u++) {
+        const int ch = 8 * u + (lane >> 3);
+        bstore16(ro, (uint32_t)(ch * plane_h + q * 8) * 2u, ld16(&st[st_off(ch, q * 8)]));
+      }
+    } else {
+      const size_t row0 = ((size_t)bi * CL + ch_base) * L + line;  // this wave's first channel row
+      const rsrc_t ro = make_rsrc((is_b ? p.b : p.a) + row0 * p.ld + pos0);
+      const bool okq = pos0 + q * 8 < p.ld;
+#pragma unroll
+      for (int u = 0; u < CPW / 8; u++) {
+        const int ch = 8 * u + (lane >> 3);
+        const uint32_t off = okq ? (uint32_t)((size_t)ch * L * p.ld + q * 8) * 2u : kOOB;
+        bstore16(ro, off, ld16(&st[st_off(ch, q * 8)]));
+      }
     }
   };
 
@@ -224,10 +264,17 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
 }
 
 hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s) {
-  if (a.mask)
-    hipLaunchKernelGGL(tmu_project_kernel<true>, dim3(grid), dim3(NW * 64), 0, s, a);
-  else
-    hipLaunchKernelGGL(tmu_project_kernel<false>, dim3(grid), dim3(NW * 64), 0, s, a);
+  if (a.frag) {
+    if (a.mask)
+      hipLaunchKernelGGL((tmu_project_kernel<true, true>), dim3(grid), dim3(NW * 64), 0, s, a);
+    else
+      hipLaunchKernelGGL((tmu_project_kernel<false, true>), dim3(grid), dim3(NW * 64), 0, s, a);
+  } else {
+    if (a.mask)
+      hipLaunchKernelGGL((tmu_project_kernel<true, false>), dim3(grid), dim3(NW * 64), 0, s, a);
+    else
+      hipLaunchKernelGGL((tmu_project_kernel<false, false>), dim3(grid), dim3(NW * 64), 0, s, a);
+  }
   return hipGetLastError();
 }
 

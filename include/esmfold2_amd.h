@@ -51,9 +51,11 @@ const char* esm_version(void);
 const char* esm_source_hash(void);
 
 /* Bytes of caller-provided workspace tmu_forward needs for B x L x L cells with
- * c latent channels: two operands [B, c, L, ld] and the contraction output
- * [B, c, L, ld], fp16, with ld = tmu_leading_dim(L); for c != 128 (the wide path) a
- * fourth plane holds LN_in(z). Each plane starts 256-byte aligned. */
+ * c latent channels: the two operands and the contraction output [B, c, L, ld], fp16,
+ * with ld = tmu_leading_dim(L), each plane sized for the larger of that layout and the
+ * MFMA-fragment layout the operands take inside tmu_forward (per channel
+ * ceil(L/32) x ceil(L/16) tiles of 512 halfs); for c != 128 (the wide path) a fourth
+ * plane holds LN_in(z). Each plane starts 256-byte aligned. */
 size_t tmu_workspace_bytes(int B, int L, int c);
 
 /* Padded row length (elements) of the channel-major operands: L rounded up to 8,

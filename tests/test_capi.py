@@ -41,9 +41,11 @@ def test_every_declared_symbol_is_exported_and_bound(pkg, lib):
 def test_version_and_sizes(lib):
     assert b"gfx950" in lib.esm_version()
     assert lib.tmu_leading_dim(238) == 240 and lib.tmu_leading_dim(240) == 240 and lib.tmu_leading_dim(1) == 8
-    # 3 planes of B*c*L*ld fp16, each rounded to 256 bytes
-    plane = 1 * 128 * 238 * 240 * 2
+    # 3 planes, each B*c times the larger of L*ld and the fragment layout's rbn*kbn*512
+    # halfs (L=238: 8 x 15 tiles of 32 rows x 16 k), fp16, rounded to 256 bytes
+    plane = 1 * 128 * max(238 * 240, 8 * 15 * 512) * 2
     assert lib.tmu_workspace_bytes(1, 238, 128) == 3 * ((plane + 255) // 256 * 256)
+    assert lib.tmu_workspace_bytes(1, 256, 128) == 3 * 128 * 256 * 256 * 2   # both layouts 256 x 256
     assert lib.tmu_workspace_bytes(0, 238, 128) == 0
 
 
@@ -86,7 +88,7 @@ def test_rejects_null_and_bad_shapes(lib):
                                   None, 0, None) == -1
     assert lib.pair_transition_workspace_bytes(1, 8, 128, 512, 0) == 0       # the register-resident kernel
     assert lib.pair_transition_workspace_bytes(1, 8, 128, 512, 1) == 2 * 8 * 8 * 128 + 2 * 8 * 8 * 512
-    assert lib.tmu_workspace_bytes(1, 8, 256) == 4 * 256 * 8 * 8 * 2  # a, b, x and LN_in(z)
+    assert lib.tmu_workspace_bytes(1, 8, 256) == 4 * 256 * 512 * 2  # a, b, x and LN_in(z); one fragment tile
     assert lib.pair_transition(None, None, None, None, 1e-5, None, None, None, 0, 8, 128, 512, None) == 0
     # the partials entry points: a NULL split count, a short buffer, a bad split count
     assert lib.q8_linear_partials(None, None, None, None, None, None, 0, None, 4, 128, 64, 64, None) == -1
