@@ -2,7 +2,10 @@
 
 A step is one TMU pair on the pair tensor z [1, 238, 238, 128] fp16:
 z1 = z + T_out(z), z2 = z1 + T_in(z1): six kernels (a, b, c per direction), inputs
-resident in HBM. value = L^2 / t_step (cells/s).
+resident in HBM. value = L^2 / t_step (cells/s). The step makes the launches
+TriMulPair / tmu_forward make (a and b in the MFMA-fragment layout, through
+tmu_project_frag and tmu_contract_frag, so that each launch can be timed on its own),
+and checks that their output equals TriMulPair's bit for bit.
 
 Also reported on the same JSON line:
   roofline      for the kernel with the largest share of the step (achieved =
@@ -223,20 +226,22 @@ def main():
     ld = K.leading_dim(L)
     z0 = z.to(dev)
     zbuf = z0.clone()
-    a = torch.empty(1, CL, L, ld, dtype=torch.float16, device=dev)
+    # the launches TriMul / tmu_forward make at C = 128: a, b in the MFMA-fragment layout
+    fp = int(lib.tmu_frag_plane_elems(L))
+    a = torch.empty(CL, fp, dtype=torch.float16, device=dev)
     b = torch.empty_like(a)
-    x = torch.empty_like(a)
+    x = torch.empty(1, CL, L, ld, dtype=torch.float16, device=dev)
     stream = torch.cuda.current_stream()
     scale = 1.0 / 256.0
 
     def launch(kind, m: "pkg.trimul.TriMul", zin, zout):
         sp = pkg.capi.stream_ptr()  # the current stream: the capture stream while a graph records
         if kind == "project":
-            rc = lib.tmu_project(zin.data_ptr(), None, m.ln_in_w.data_ptr(), m.ln_in_b.data_ptr(), m.ln_in_eps,
-                                 m.w_bundle.data_ptr(), a.data_ptr(), b.data_ptr(), 1, L, C, CL, ld,
-                                 int(not m.outgoing), sp)
+            rc = lib.tmu_project_frag(zin.data_ptr(), None, m.ln_in_w.data_ptr(), m.ln_in_b.data_ptr(), m.ln_in_eps,
+                                      m.w_bundle.data_ptr(), a.data_ptr(), b.data_ptr(), 1, L, C, CL,
+                                      int(not m.outgoing), sp)
         elif kind == "contract":
-            rc = lib.tmu_contract(a.data_ptr(), b.data_ptr(), x.data_ptr(), CL, L, ld, ld, scale, sp)
+            rc = lib.tmu_contract_frag(a.data_ptr(), b.data_ptr(), x.data_ptr(), CL, L, ld, scale, sp)
         else:
             rc = lib.tmu_epilogue(x.data_ptr(), ld, zin.data_ptr(), None, m.ln_in_w.data_ptr(), m.ln_in_b.data_ptr(),
                                   m.ln_in_eps, m.ln_mix_w.data_ptr(), m.ln_mix_b.data_ptr(),
@@ -259,6 +264,10 @@ def main():
     pair_out = zbuf.cpu()
     if not torch.isfinite(pair_out.float()).all():
         raise SystemExit("TMU pair output is not finite")
+    # the same launches as the module's own path (TriMulPair -> tmu_forward): the same bits
+    via_module = pkg.trimul.TriMulPair(t_out, t_in)(z0).cpu()
+    if not torch.equal(via_module.view(torch.int16), pair_out.view(torch.int16)):
+        raise SystemExit("the timed launches differ from TriMulPair's output")
 
     for _ in range(args.warmup):
         step()
@@ -314,16 +323,17 @@ def main():
                    "mfma_frac": counts[k]["flops"] / t / MFMA_F16_PEAK,
                    "hbm_frac": counts[k]["bytes"] / t / HBM_PEAK}
     traffic = measured_traffic()
+    kname = {"project": "tmu_project_kernel", "contract": "tmu_contract_frag_kernel", "epilogue": "tmu_epilogue_kernel"}
     for k in kinds:
-        kern[k]["traffic_bytes"] = traffic.get(f"tmu_{k}_kernel")
+        kern[k]["traffic_bytes"] = traffic.get(kname[k])
     dom = max(kinds, key=lambda k: kern[k]["us"])
     if dom == "contract":
         roof = {"bound": "mfma", "achieved": kern[dom]["tflops"], "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
-                "frac": kern[dom]["mfma_frac"], "traffic": kern[dom]["traffic_bytes"], "kernel": "tmu_contract_kernel",
+                "frac": kern[dom]["mfma_frac"], "traffic": kern[dom]["traffic_bytes"], "kernel": kname[dom],
                 "per_launch": f"{counts[dom]['flops'] / 1e9:.3f} GFLOP"}
     else:
         roof = {"bound": "hbm", "achieved": kern[dom]["gbs"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": kern[dom]["hbm_frac"], "traffic": kern[dom]["traffic_bytes"], "kernel": f"tmu_{dom}_kernel",
+                "frac": kern[dom]["hbm_frac"], "traffic": kern[dom]["traffic_bytes"], "kernel": kname[dom],
                 "per_launch": f"{counts[dom]['bytes'] / 1e6:.2f} MB"}
 
     pair_flops = 2 * sum(v["flops"] for v in counts.values())

@@ -25,6 +25,9 @@ SIGNATURES = {
     "tmu_leading_dim": (_int, [_int]),
     "tmu_project": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp]),
     "tmu_contract": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _f32, _vp]),
+    "tmu_frag_plane_elems": (_sz, [_int]),
+    "tmu_project_frag": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
+    "tmu_contract_frag": (_int, [_vp, _vp, _vp, _int, _int, _int, _f32, _vp]),
     "tmu_epilogue": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int,
                             _int, _int, _int, _vp]),
     "tmu_forward": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _int, _int, _int,

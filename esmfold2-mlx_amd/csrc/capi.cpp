@@ -158,6 +158,31 @@ int tmu_project(const esm_half* z, const esm_half* mask, const float* ln_w, cons
   return project_impl(z, mask, ln_w, ln_b, ln_eps, w, a_out, b_out, B, L, C, c, ld, incoming, false, stream);
 }
 
+size_t tmu_frag_plane_elems(int L) { return L <= 0 ? 0 : esm::FragLayout::plane_halfs(L); }
+
+int tmu_project_frag(const esm_half* z, const esm_half* mask, const float* ln_w, const float* ln_b, float ln_eps,
+                     const esm_half* w, esm_half* a_out, esm_half* b_out, int B, int L, int C, int c,
+                     int incoming, void* stream) {
+  return project_impl(z, mask, ln_w, ln_b, ln_eps, w, a_out, b_out, B, L, C, c, tmu_leading_dim(L), incoming, true,
+                      stream);
+}
+
+int tmu_contract_frag(const esm_half* a, const esm_half* b, esm_half* x, int batch, int L, int ldx, float scale,
+                      void* stream) {
+  if (batch < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_contract_frag: batch=%d L=%d must be >= 0", batch, L);
+  if (batch == 0 || L == 0) return ok();
+  if (!a || !b || !x) return fail(ESM_ERR_NULL, "tmu_contract_frag: NULL pointer");
+  if (L > kMaxL || batch > 65535)
+    return fail(ESM_ERR_SHAPE, "tmu_contract_frag: L=%d batch=%d out of range", L, batch);
+  if (ldx % 8 != 0 || ldx < L || ldx > round_up(L, 32))
+    return fail(ESM_ERR_SHAPE, "tmu_contract_frag: ldx=%d must be a multiple of 8 in [L, roundup(L, 32)] (L=%d)", ldx,
+                L);
+  if (!aligned16(a) || !aligned16(b) || !aligned16(x))
+    return fail(ESM_ERR_ALIGN, "tmu_contract_frag: a, b, x must be 16-byte aligned");
+  esm::ContractArgs args{H(a), H(b), H(x), batch, L, 0, ldx, scale, 1};
+  return hip_status(esm::launch_contract(args, (hipStream_t)stream), "tmu_contract_frag launch");
+}
+
 int tmu_contract(const esm_half* a, const esm_half* b, esm_half* x, int batch, int L, int ld, int ldx, float scale,
                  void* stream) {
   if (batch < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_contract: batch=%d L=%d must be >= 0", batch, L);
@@ -314,9 +339,7 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
   int rc = project_impl(z, mask, ln_in_w, ln_in_b, ln_in_eps, w_bundle, wa, wb, B, L, C, c, ld, outgoing ? 0 : 1,
                         true, stream);
   if (rc) return rc;
-  if (B * c > 65535) return fail(ESM_ERR_SHAPE, "tmu_forward: B=%d too large", B);
-  esm::ContractArgs ca{H(wa), H(wb), H(wx), B * c, L, ld, ld, kScale, 1};
-  rc = hip_status(esm::launch_contract(ca, (hipStream_t)stream), "tmu_forward contract launch");
+  rc = tmu_contract_frag(wa, wb, wx, B * c, L, ld, kScale, stream);
   if (rc) return rc;
   return tmu_epilogue(wx, ld, z, mask, ln_in_w, ln_in_b, ln_in_eps, ln_mix_w, ln_mix_b, ln_mix_eps * kScale * kScale,
                       w_emit, w_gate, out, B, L, C, c, residual, out_mask, stream);

@@ -159,5 +159,11 @@ DEV void ln_row128(float (&v)[8], const float (&g)[8], const float (&b)[8], floa
   }
   const float rstd = rsqrtf(row16_sum(q) * (1.0f / 128.0f) + eps);
 #pragma unroll
-  for (int e = 0; e < 8; e++) v[e] = v[e] * rstd * g[e] + b[e];
+  for (int e = 0; e < 8; e++) {
+    v[e] = v[e] * rstd * g[e] + b[e];
+    // The fp32 result is materialised: otherwise the compiler may fold the caller's fp16
+    // conversion into the last FMA (one rounding) in one inlined copy and not in another
+    // (fp32 then fp16), and the same cell would round differently by tile position.
+    __asm__ volatile("" : "+v"(v[e]));
+  }
 }

@@ -108,6 +108,27 @@ int tmu_contract(const esm_half* a, const esm_half* b, esm_half* x, int batch, i
                  void* stream);
 
 /*
+ * Kernels (a) and (b) with the operands in the MFMA-fragment layout tmu_forward uses
+ * internally at C = c = 128 (the same launches, exposed so that a caller can run or
+ * time them one at a time; the results are bit-identical to tmu_project + tmu_contract).
+ * The layout, per channel plane: ceil(L/32) x ceil(L/16) tiles of 64 lanes x 8 fp16,
+ * tile (rb, kb) lane l holding operand row 32 rb + l % 32, k = 16 kb + 8 (l / 32) .. +7
+ * (tmu_frag_plane_elems(L) elements; rows at or past L are left unwritten and never read,
+ * k at or past L is zero). Same reference interfaces as tmu_project and tmu_contract.
+ *
+ * tmu_project_frag: z, mask, LN and weights as tmu_project; a_out, b_out [B * c] planes.
+ * tmu_contract_frag: a, b [batch] planes; x [batch, L, ldx] as tmu_contract, columns
+ *   [L, ldx) written with zeros; ldx % 8 == 0, L <= ldx <= roundup(L, 32).
+ * Supported: C = c = 128 (project). Pointers 16-byte aligned.
+ */
+size_t tmu_frag_plane_elems(int L);
+int tmu_project_frag(const esm_half* z, const esm_half* mask, const float* ln_w, const float* ln_b, float ln_eps,
+                     const esm_half* w, esm_half* a_out, esm_half* b_out, int B, int L, int C, int c,
+                     int incoming, void* stream);
+int tmu_contract_frag(const esm_half* a, const esm_half* b, esm_half* x, int batch, int L, int ldx, float scale,
+                      void* stream);
+
+/*
  * Kernel (c): norm_mix LayerNorm over c of the channel-major contraction ->
  * proj_emit -> * sigmoid(proj_gate(LN_in(z))) [-> * mask] [-> + z], written
  * cell-major.

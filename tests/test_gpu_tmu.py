@@ -123,6 +123,50 @@ def test_contract_kernel(gpu_lib, pkg, L):
     assert float(((got - ref).abs() > ref.abs() * 2.0 ** -10 + 2.0 ** -24).double().mean()) < 1e-3
 
 
+def _frag_to_rows(planes, L):
+    """[n, rbn*kbn*512] fragment-layout planes -> [n, L, L] row-major (rows and k past L
+    dropped): tile (rb, kb), lane l holds row 32 rb + l % 32, k = 16 kb + 8 (l // 32) .. +7."""
+    n = planes.shape[0]
+    rbn, kbn = (L + 31) // 32, (L + 15) // 16
+    t = planes.view(n, rbn, kbn, 2, 32, 8)            # [n, rb, kb, l // 32, l % 32, e]
+    rows = t.permute(0, 1, 4, 2, 3, 5).reshape(n, 32 * rbn, 16 * kbn)
+    return rows[:, :L, :L], rows[:, :L, L:]
+
+
+@pytest.mark.parametrize("L", [1, 17, 33, 100, 238])
+@pytest.mark.parametrize("incoming", [False, True])
+def test_fragment_layout_path_matches_row_major(gpu_lib, pkg, L, incoming):
+    # tmu_project_frag + tmu_contract_frag (the launches tmu_forward makes at C = 128) against
+    # tmu_project + tmu_contract: the same operand values in the other layout, zeros for k
+    # past L, and the contraction bit for bit
+    lib, K = pkg.capi.lib(), pkg.kernels
+    p = _weights(L + 5, not incoming, random_ln=True)
+    z, mask = _z(L, 2, L), _mask(L + 1, 2, L, "random")
+    zd, md = z.to(DEV), mask.to(DEV)
+    w = p.w_bundle.half().to(DEV)
+    lw, lb = p.ln_in_w.to(DEV), p.ln_in_b.to(DEV)
+    a, b = K.project(zd, md, lw, lb, p.ln_in_eps, w, incoming)
+    fp = int(lib.tmu_frag_plane_elems(L))
+    af = torch.full((2 * 128, fp), float("nan"), dtype=torch.float16, device=DEV)  # rows past L stay NaN
+    bf = af.clone()
+    pkg.capi.check(lib.tmu_project_frag(zd.data_ptr(), md.data_ptr(), lw.data_ptr(), lb.data_ptr(), p.ln_in_eps,
+                                        w.data_ptr(), af.data_ptr(), bf.data_ptr(), 2, L, 128, 128, int(incoming),
+                                        pkg.capi.stream_ptr()))
+    ld = K.leading_dim(L)
+    x = K.contract(a, b, L, scale=1 / 256)
+    xf = torch.empty(2 * 128, L, ld, dtype=torch.float16, device=DEV)
+    pkg.capi.check(lib.tmu_contract_frag(af.data_ptr(), bf.data_ptr(), xf.data_ptr(), 2 * 128, L, ld, 1 / 256,
+                                         pkg.capi.stream_ptr()))
+    torch.cuda.synchronize()
+    for got, ref in ((af, a), (bf, b)):
+        vals, pad_k = _frag_to_rows(got.cpu(), L)
+        kpad = min(16 * ((L + 15) // 16), 8 * ((L + 7) // 8)) - L  # k past L written by the 8 x 8 tiles
+        assert torch.equal(vals.view(torch.int16), ref.cpu().reshape(2 * 128, L, ld)[..., :L].view(torch.int16))
+        assert torch.count_nonzero(pad_k[..., :kpad]) == 0
+    assert torch.equal(xf.view(torch.int16), x.reshape(2 * 128, L, ld).view(torch.int16))
+    assert torch.isfinite(xf).all()
+
+
 @pytest.mark.parametrize("L", [5, 64, 100])
 @pytest.mark.parametrize("residual", [False, True])
 def test_epilogue_kernel(gpu_lib, pkg, L, residual):
