@@ -244,7 +244,7 @@ static int tmu_forward_wide(const esm_half* z, const esm_half* mask, const float
   const int ld = tmu_leading_dim(L);
   const size_t ncell = (size_t)B * L * L;
   if (ncell * C * 2 >= (1ull << 31)) return fail(ESM_ERR_SHAPE, "tmu_forward: B*L*L*C=%zu exceeds 2^30", ncell * C);
-  const size_t plane = (size_t)B * c * L * ld;
+  const size_t plane = (size_t)B * c * tmu_plane_halfs(L);
   const size_t a256 = (plane * sizeof(esm_half) + 255) / 256 * 256 / sizeof(esm_half);
   half_t* wa = static_cast<half_t*>(workspace);
   half_t* wb = wa + a256;
@@ -268,10 +268,19 @@ static int tmu_forward_wide(const esm_half* z, const esm_half* mask, const float
   g.plane_b = wb;
   g.c = c;
   g.ld = ld;
+  // K = C <= 256 runs the weight-stationary GEMM, which writes a, b in the fragment layout
+  // (the contraction then reads each operand fragment straight into registers)
+  const bool frag = C <= 256;
+  if (frag) {
+    g.frag = 1;
+    g.rbn = (L + 31) / 32;
+    g.kbn = (L + 15) / 16;
+  }
   if (esm::wide_gemm_blocks(g) > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_forward: too many tiles");
   e = esm::launch_wide_gemm(g, esm::kWideGateCM, st, cu_count());
   if (e != hipSuccess) return hip_status(e, "tmu_forward gate launch");
-  esm::ContractArgs ca{wa, wb, wx, B * c, L, ld, ld, kScale};
+  if (B * c > 65535) return fail(ESM_ERR_SHAPE, "tmu_forward: B=%d too large", B);
+  esm::ContractArgs ca{wa, wb, wx, B * c, L, ld, ld, kScale, frag ? 1 : 0};
   e = esm::launch_contract(ca, st);
   if (e != hipSuccess) return hip_status(e, "tmu_forward contract launch");
   e = esm::launch_ln_cf_to_cl(wx, ld, ln_mix_w, ln_mix_b, ln_mix_eps * kScale * kScale, wa, B, L, c, st);

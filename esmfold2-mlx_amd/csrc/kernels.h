@@ -174,6 +174,8 @@ struct WideArgs {
   int B, L;             // cells = B * L * L, tiled along lines of L cells
   int tiles_per_line;   // ceil(L / 128)
   int transpose;        // 1: line = column, positions along rows (the incoming operands)
+  int frag;             // GATE_CM with K <= 256: a, b planes in FragLayout, tiles of 8 x 8 cells
+  int rbn, kbn;         // FragLayout tiles per plane (frag)
   half_t* out;          // [cells, ldo] cell-major output (all but GATE_CM)
   int ldo;
   const half_t* z;      // [cells, ldo] residual (RESGATE with residual, RESID)

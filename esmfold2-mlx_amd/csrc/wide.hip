@@ -366,7 +366,9 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
             const size_t cell = cell0 + (size_t)c_e * cstride;
             const float zv = wide_needs_z<EPI>() && in && (EPI == kWideResid || p.residual)
                                  ? (float)p.z[cell * p.ldo + n0 + o_e] : 0.f;
-            hv[mi][ni][g4][e] = (half_t)wide_value<EPI>(p, acc[mi][ni][4 * g4 + e], d2[e], cell, in, zv);
+            float v = wide_value<EPI>(p, acc[mi][ni][4 * g4 + e], d2[e], cell, in, zv);
+            __asm__ volatile("" : "+v"(v));  // fp32 then fp16 at every position (as the weight-stationary form)
+            hv[mi][ni][g4][e] = (half_t)v;
           }
         }
   }
@@ -447,7 +449,10 @@ DEV float wide_value_u(const WideArgs& p, float d1, float d2, size_t cell, bool 
   return v;
 }
 
-template <int EPI, bool DUAL, bool A2SEP, int KW>  // KW = K / 16
+// FRAG (the channel-major epilogue only): tiles of 8 x 8 cells, operand rows line .. line+7
+// by k pos0 .. pos0+7 (tile cell c = 8 dr + dc), and the a, b planes written in FragLayout,
+// one whole 128-byte segment per channel and tile.
+template <int EPI, bool DUAL, bool A2SEP, int KW, bool FRAG = false>
 __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   constexpr int K = 16 * KW;
   constexpr int KS = K / 32;                    // k-steps of the 16x16x32 MFMA
@@ -467,6 +472,7 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   static_assert(CH_A >= 1 && SBM * (K / 8) % WNT == 0, "whole loads per thread");
   static_assert(KS >= 1 && K % 32 == 0, "K a multiple of 32");
   static_assert(!(CM && ZR), "no residual with channel-major planes");
+  static_assert(!FRAG || CM, "the fragment layout is for the channel-major planes");
   __shared__ __align__(16) char smem_c[SMEM_BYTES];
   half_t* a_s = reinterpret_cast<half_t*>(smem_c);
   half_t* os = reinterpret_cast<half_t*>(smem_c + A_HALFS * 2);
@@ -480,8 +486,8 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   const int slice = lg % S;
   const int n0 = slice * BN;
   const int stride = gridDim.x / S;             // tile groups
-  const int tpl = (L + SBM - 1) / SBM;
-  const int ntiles = p.B * L * tpl;
+  const int tpl = FRAG ? (L + 7) / 8 : (L + SBM - 1) / SBM;  // FRAG: tiles per dimension
+  const int ntiles = FRAG ? p.B * tpl * tpl : p.B * L * tpl;
   // first output (in the slice) of 16-output block b of this wave
   const int ob0 = DUAL ? 16 * wave : 32 * wave;
 
@@ -493,13 +499,32 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   const rsrc_t rZ = make_rsrc(ZR ? (const void*)p.z : (const void*)p.a1);
   auto tile_coords = [&](int tile_v, int& bi, int& line, int& pos0) {
     const int tile = __builtin_amdgcn_readfirstlane(tile_v);  // uniform: keep the division scalar
-    const int bl = tile / tpl;
-    pos0 = (tile - bl * tpl) * SBM;
-    bi = bl / L;
-    line = bl - bi * L;
+    if constexpr (FRAG) {
+      bi = tile / (tpl * tpl);
+      const int t = tile - bi * tpl * tpl, tr = t / tpl;
+      line = 8 * tr;
+      pos0 = 8 * (t - tr * tpl);
+    } else {
+      const int bl = tile / tpl;
+      pos0 = (tile - bl * tpl) * SBM;
+      bi = bl / L;
+      line = bl - bi * L;
+    }
   };
   auto cell_of = [&](int bi, int line, int pos) -> size_t {
     return p.transpose ? ((size_t)bi * L + pos) * L + line : ((size_t)bi * L + line) * L + pos;
+  };
+  // tile cell c: its (line, position) and whether it lies inside the grid
+  auto tcell = [&](int line, int pos0, int c, int& ln, int& ps) -> bool {
+    if constexpr (FRAG) {
+      ln = line + (c >> 3);
+      ps = pos0 + (c & 7);
+      return ln < L && ps < L;
+    } else {
+      ln = line;
+      ps = pos0 + c;
+      return ps < L;
+    }
   };
   struct Regs {
     half8 a[NA][CH_A];
@@ -514,8 +539,9 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
 #pragma unroll
     for (int u = 0; u < CH_A; u++) {
       const int id = tid + WNT * u, row = id / (K / 8), j = id - row * (K / 8);
-      const bool ok = live && pos0 + row < L;
-      const uint32_t off = ok ? (uint32_t)(cell_of(bi, line, pos0 + row) * K + 8 * j) * 2u : kOOB;
+      int ln, ps;
+      const bool ok = tcell(line, pos0, row, ln, ps) && live;
+      const uint32_t off = ok ? (uint32_t)(cell_of(bi, ln, ps) * K + 8 * j) * 2u : kOOB;
       r.a[0][u] = bload16(rA1, off);
       if constexpr (A2SEP) r.a[1][u] = bload16(rA2, off);
     }
@@ -576,10 +602,20 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
           for (int e = 0; e < 4; e++) {
             const int cl = CM ? 16 * cb + 4 * q4 + e : 16 * cb + l16;
             const int ol = CM ? ob0 + l16 : ob0 + 16 * b + 4 * q4 + e;
-            const bool in = cl < nvalid && n0 + ol < p.N;
+            int ln, ps;
+            const bool in = (FRAG ? tcell(line, pos0, cl, ln, ps) : cl < nvalid) && n0 + ol < p.N;
+            if constexpr (!FRAG) {
+              ln = line;
+              ps = pos0 + cl;
+            }
             const float d1 = acc[DUAL ? 0 : b][cb][e], d2 = DUAL ? acc[1][cb][e] : 0.f;
             const float zv = ZR ? (float)ra.z[ZR ? b : 0][ZR ? cb : 0][e] : 0.f;  // zeros past the ends
-            hv[e] = (half_t)wide_value_u<EPI, HM, RS>(p, d1, d2, HM ? cell_of(bi, line, pos0 + cl) : 0, in, zv);
+            float v = wide_value_u<EPI, HM, RS>(p, d1, d2, HM ? cell_of(bi, ln, ps) : 0, in, zv);
+            // fp32 first, then fp16, at every position: left to itself the compiler fuses the
+            // last multiply with the conversion (one rounding) at some accumulator positions
+            // only, so a cell's bits would depend on where the tiling puts it
+            __asm__ volatile("" : "+v"(v));
+            hv[e] = (half_t)v;
           }
           if (CM)
             *reinterpret_cast<half4*>(os + (ob0 + l16) * OS + 16 * cb + 4 * q4) = hv;
@@ -597,7 +633,21 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
       if (rs) finish(F_{}, T_{}); else finish(F_{}, F_{});
     }
     __syncthreads();  // the staged tile is complete; every wave is done with the A tiles
-    if constexpr (CM) {
+    if constexpr (CM && FRAG) {
+      // chunk q of a channel's staged row: operand row line + q, k pos0 .. pos0+7, lane
+      // (line + q) % 32 + 32 (pos0 / 8 % 2) of tile ((line + q) / 32, pos0 / 16)
+      const size_t plane_h = (size_t)p.rbn * p.kbn * FragLayout::kTileHalfs;
+      const size_t tile_h = ((size_t)(line >> 5) * p.kbn + (pos0 >> 4)) * FragLayout::kTileHalfs +
+                            (size_t)((line & 31) + 32 * ((pos0 >> 3) & 1)) * 8;
+      for (int id = tid; id < BN * (SBM / 8); id += WNT) {
+        const int o = id / (SBM / 8), q = id - o * (SBM / 8);
+        const int n = n0 + o;
+        if (n >= p.N) continue;
+        half_t* plane = n < p.c ? p.plane_a : p.plane_b;
+        const int ch = n < p.c ? n : n - p.c;
+        st16(plane + ((size_t)bi * p.c + ch) * plane_h + tile_h + 8 * q, ld16(os + o * OS + 8 * q));
+      }
+    } else if constexpr (CM) {
       for (int id = tid; id < BN * (SBM / 8); id += WNT) {
         const int o = id / (SBM / 8), q = id - o * (SBM / 8);
         const int n = n0 + o;
@@ -731,7 +781,8 @@ static hipError_t launch_wide_gemm_ws(const WideArgs& a, int epi, int cus, hipSt
   const bool dual = a.w2 != nullptr, sep = a.a2 != nullptr && a.a2 != a.a1;
   const int bn = dual ? 128 : 256;
   const int S = (a.N + bn - 1) / bn;
-  const long long tiles = (long long)a.B * a.L * ((a.L + SBM - 1) / SBM);
+  const long long tpd = (a.L + 7) / 8;
+  const long long tiles = a.frag ? a.B * tpd * tpd : (long long)a.B * a.L * ((a.L + SBM - 1) / SBM);
   long long groups = (cus > S ? cus : S) / S;   // one workgroup per CU
   groups -= groups % kNumXcd == 0 || groups < kNumXcd ? 0 : groups % kNumXcd;
   if (groups > tiles) groups = tiles;
@@ -740,7 +791,10 @@ static hipError_t launch_wide_gemm_ws(const WideArgs& a, int epi, int cus, hipSt
   switch (epi) {                                                                                             \
     case kWideGateCM:                                                                                        \
       if (!dual || sep) return hipErrorInvalidValue;                                                         \
-      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideGateCM, true, false, KW>), grid, block, 0, s, a);         \
+      if (a.frag)                                                                                            \
+        hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideGateCM, true, false, KW, true>), grid, block, 0, s, a); \
+      else                                                                                                   \
+        hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideGateCM, true, false, KW>), grid, block, 0, s, a);       \
       break;                                                                                                 \
     case kWideResGate:                                                                                       \
       if (!dual || !sep) return hipErrorInvalidValue;                                                        \
@@ -772,6 +826,7 @@ static hipError_t launch_wide_gemm_ws(const WideArgs& a, int epi, int cus, hipSt
 
 hipError_t launch_wide_gemm(const WideArgs& a, int epi, hipStream_t s, int cus) {
   if ((a.K == 128 || a.K == 256) && cus > 0) return launch_wide_gemm_ws(a, epi, cus, s);
+  if (a.frag) return hipErrorInvalidValue;  // the fragment layout is written by the weight-stationary form only
   const dim3 grid((unsigned)wide_gemm_blocks(a)), block(WNT);
   const bool dual = a.w2 != nullptr, sep = a.a2 != nullptr && a.a2 != a.a1;
   switch (epi) {
