@@ -1,5 +1,5 @@
 // Shared device helpers for the gfx950 (CDNA4) kernels: vector types, MFMA
-// wrappers, 16-lane LayerNorm reductions and fp16 packing.
+// wrappers, LayerNorm statistics and reductions, buffer access and weight staging.
 //
 // MFMA lane layouts used throughout (checked on an MI355X by an in-bounds
 // probe before any kernel relied on them):
@@ -144,26 +144,58 @@ DEV float sigmoidf_fast(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
-// LayerNorm of one 8-channel slice held by this lane, where the 16 lanes of a
-// DPP row together hold one 128-channel row. Statistics in fp32, two-pass.
-DEV void ln_row128(float (&v)[8], const float (&g)[8], const float (&b)[8], float eps) {
-  float s = 0.f;
+// --- LayerNorm from fp16 inputs, three VALU operations per value ----------------------
+// Sums of the values and of their squares, accumulated in fp32: v_dot2_f32_f16 forms two
+// exact fp16 products per instruction (the sum: products with 1).
+DEV void dot2_moments(half8 v, float& s, float& q) {
+  const half2v one = {(half_t)1.0f, (half_t)1.0f};
 #pragma unroll
-  for (int e = 0; e < 8; e++) s += v[e];
-  const float mean = row16_sum(s) * (1.0f / 128.0f);
-  float q = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    v[e] -= mean;
-    q += v[e] * v[e];
+  for (int p = 0; p < 4; p++) {
+    const half2v x = {v[2 * p], v[2 * p + 1]};
+    s = __builtin_amdgcn_fdot2(x, one, s, false);
+    q = __builtin_amdgcn_fdot2(x, x, q, false);
   }
-  const float rstd = rsqrtf(row16_sum(q) * (1.0f / 128.0f) + eps);
+}
+DEV void dot2_moments(half4 v, float& s, float& q) {
+  const half2v one = {(half_t)1.0f, (half_t)1.0f};
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    v[e] = v[e] * rstd * g[e] + b[e];
-    // The fp32 result is materialised: otherwise the compiler may fold the caller's fp16
-    // conversion into the last FMA (one rounding) in one inlined copy and not in another
-    // (fp32 then fp16), and the same cell would round differently by tile position.
-    __asm__ volatile("" : "+v"(v[e]));
+  for (int p = 0; p < 2; p++) {
+    const half2v x = {v[2 * p], v[2 * p + 1]};
+    s = __builtin_amdgcn_fdot2(x, one, s, false);
+    q = __builtin_amdgcn_fdot2(x, x, q, false);
   }
+}
+// rstd = 1 / sqrt(var + eps) and shift = -mean * rstd from the sums over n values, with
+// var = E[x^2] - E[x]^2 in fp32 (clamped at 0). Against the two-pass form this loses about
+// n 2^-24 (1 + mean^2 / var) of var: below the fp16 rounding of the result while |mean| is
+// within 8 standard deviations of a row.
+DEV void ln_scale_shift(float s, float q, float inv_n, float eps, float& rstd, float& shift) {
+  const float mean = s * inv_n;
+  const float var = fmaxf(fmaf(q, inv_n, -mean * mean), 0.f);
+  rstd = rsqrtf(var + eps);
+  shift = -mean * rstd;
+}
+// One normalised value, (x - mean) rstd gamma + beta, from its fp16 input (v_fma_mix_f32
+// reads the fp16 operand directly), rounded once to fp16. The fp32 result is materialised
+// first: otherwise the compiler may fold the conversion into the last FMA in one inlined
+// copy and not in another, and the same value would round differently by position.
+DEV half_t ln_value(half_t x, float rstd, float shift, float g, float b) {
+  float y = fmaf(fmaf((float)x, rstd, shift), g, b);
+  __asm__ volatile("" : "+v"(y));
+  return (half_t)y;
+}
+
+// LayerNorm of one 8-channel slice held by this lane, where the 16 lanes of a DPP row
+// together hold one 128-channel row: fp16 in, fp16 out, fp32 statistics (dot2_moments).
+DEV half8 ln_row128_h(half8 x, const float (&g)[8], const float (&b)[8], float eps) {
+  float s = 0.f, q = 0.f;
+  dot2_moments(x, s, q);
+  s = row16_sum(s);
+  q = row16_sum(q);
+  float rstd, shift;
+  ln_scale_shift(s, q, 1.0f / 128.0f, eps, rstd, shift);
+  half8 o;
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = ln_value(x[e], rstd, shift, g[e], b[e]);
+  return o;
 }

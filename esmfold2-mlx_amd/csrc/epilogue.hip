@@ -20,7 +20,7 @@
 //      lane reads the B-fragment chunks of its cell; z stays staged for the residual;
 //   3. both LayerNorms run in registers on the fragments: a lane holds 64 of its
 //      cell's 128 channels and its partner lane (lane ^ 32) the other 64, so the
-//      statistics are a lane-local sum plus one exchange (fp32, shifted one-pass);
+//      statistics are a lane-local sum plus one exchange (fp32 sums from v_dot2_f32_f16);
 //   4. D[o][cell] = W_e[o,:] . LN(x)[cell,:] and the gate GEMM on LN(z) with
 //      v_mfma_f32_32x32x16_f16, A-fragments read from the LDS-resident weights, two
 //      passes of two 32-row output blocks (4 independent accumulator chains each);
@@ -64,32 +64,17 @@ DEV half4 tr_read(const half_t* xs, int k0, int n0, int lane) {
 
 // LayerNorm of one cell's 128 channels held as MFMA B-fragments: this lane holds channels
 // 16 s + 8 h + e (s = 0..7, e = 0..7, h = lane / 32), the partner lane (lane ^ 32) the
-// other half. Statistics in fp32 in one pass, shifted by K = one channel of the cell
-// (the same for both lanes): sums of d = x - K and d^2, mean = K + E[d],
-// var = E[d^2] - E[d]^2. With |K - mean| of the order of the standard deviation the
-// cancellation in var is that of the two-pass form, and no fp32 copy of the 64 values
-// has to stay live between passes. gamma / beta come from LDS (fp32).
+// other half. Statistics in fp32: sums of the values and of their squares with
+// v_dot2_f32_f16 (two exact fp16 products per instruction), a lane-local sum plus one
+// exchange, var = E[x^2] - E[x]^2 (ln_scale_shift). gamma / beta come from LDS (fp32).
 DEV void ln_frags(half8 (&v)[CL / 16], const float* w, const float* b, float eps, int h) {
-  const float K = __shfl((float)v[0][0], threadIdx.x & 31);
-  float s0 = 0.f, s1 = 0.f, q0 = 0.f, q1 = 0.f;
+  float s = 0.f, q = 0.f;
 #pragma unroll
-  for (int k = 0; k < CL / 16; k++)
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const float d0 = (float)v[k][e] - K, d1 = (float)v[k][e + 1] - K;
-      s0 += d0;
-      s1 += d1;
-      q0 = fmaf(d0, d0, q0);
-      q1 = fmaf(d1, d1, q1);
-    }
-  float s = s0 + s1, q = q0 + q1;
+  for (int k = 0; k < CL / 16; k++) dot2_moments(v[k], s, q);
   s += __shfl_xor(s, 32);
   q += __shfl_xor(q, 32);
-  const float md = s * (1.0f / CL);
-  const float mean = K + md;
-  const float var = fmaxf(fmaf(q, 1.0f / CL, -md * md), 0.f);
-  const float rstd = rsqrtf(var + eps);
-  const float shift = -mean * rstd;
+  float rstd, shift;
+  ln_scale_shift(s, q, 1.0f / CL, eps, rstd, shift);
 #pragma unroll
   for (int k = 0; k < CL / 16; k++) {
     const int c0 = 16 * k + 8 * h;
@@ -97,8 +82,8 @@ DEV void ln_frags(half8 (&v)[CL / 16], const float* w, const float* b, float eps
     const f32x4 b0 = *reinterpret_cast<const f32x4*>(b + c0), b1 = *reinterpret_cast<const f32x4*>(b + c0 + 4);
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      v[k][e] = (half_t)fmaf(fmaf((float)v[k][e], rstd, shift), w0[e], b0[e]);
-      v[k][e + 4] = (half_t)fmaf(fmaf((float)v[k][e + 4], rstd, shift), w1[e], b1[e]);
+      v[k][e] = ln_value(v[k][e], rstd, shift, w0[e], b0[e]);
+      v[k][e + 4] = ln_value(v[k][e + 4], rstd, shift, w1[e], b1[e]);
     }
   }
 }

@@ -20,9 +20,9 @@
 // staged per wave in LDS and leave as whole 128-byte row segments (8 lanes x 16 B
 // per channel row): scattered 32-byte pieces of rows measured 2x slower.
 //
-// Per tile: LayerNorm (16 lanes per cell) into a double-buffered LDS tile, one
-// barrier, then MFMA + gate + staging + store. The next tile's z is loaded while
-// this one computes. Every global access is an unconditional buffer
+// Per tile: LayerNorm (16 lanes per cell, v_dot2_f32_f16 statistics) into a double-buffered
+// LDS tile, one barrier, then MFMA + gate + staging + store. The next tile's z is loaded
+// while this one computes. Every global access is an unconditional buffer
 // instruction (out-of-range lanes use an offset the hardware drops), so the
 // compiler's wait counts stay exact and the prefetch stays in flight.
 #include "common.h"
@@ -157,17 +157,12 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
 #pragma unroll
     for (int it = 0; it < CPT; it++) {
       const int cl = (tid >> 4) + (NW * 4) * it;
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = (float)zq[it][e];
-      ln_row128(v, g, bb, p.eps);
+      half8 o = ln_row128_h(zq[it], g, bb, p.eps);
       // Cells past L (zeros from the range-checked loads) enter the projection as zeros,
       // so their padded outputs [L, ld) are exactly 0 with or without a mask (their
       // LayerNorm would be 0 * rsqrt(eps), NaN for eps = 0).
       const bool cell_in = cell_ok(line, pos0, cl);
-      half8 o;
-#pragma unroll
-      for (int e = 0; e < 8; e++) o[e] = cell_in ? (half_t)v[e] : (half_t)0.f;
+      if (!cell_in) o = zero_half8();
       st16(&ns[cl * NS + ch0], o);
       if (has_mask && (lane & 15) == 0) m_s[nb][cl] = cell_in ? h2f(mq[it]) : 0.f;
     }
@@ -198,14 +193,18 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
 #pragma unroll
       for (int r4 = 0; r4 < 4; r4++) {
         const int c4 = 32 * h + acc_row32(4 * r4, lane);  // first of this group's 4 cells
+        // (a padding cell's signal is already 0: zero LayerNorm row)
+        const f32x4 m4 = has_mask ? *reinterpret_cast<const f32x4*>(&m_s[nb][c4]) : f32x4{1.f, 1.f, 1.f, 1.f};
         half4 v;
-        if (has_mask) {
-          const f32x4 m4 = *reinterpret_cast<const f32x4*>(&m_s[nb][c4]);
 #pragma unroll
-          for (int e = 0; e < 4; e++) v[e] = (half_t)(as[h][4 * r4 + e] * sigmoidf_fast(ag[h][4 * r4 + e]) * m4[e]);
-        } else {  // a padding cell's signal is already 0 (zero LayerNorm row)
-#pragma unroll
-          for (int e = 0; e < 4; e++) v[e] = (half_t)(as[h][4 * r4 + e] * sigmoidf_fast(ag[h][4 * r4 + e]));
+        for (int e = 0; e < 4; e++) {
+          float t = as[h][4 * r4 + e] * sigmoidf_fast(ag[h][4 * r4 + e]);
+          if (has_mask) t *= m4[e];
+          // fp32 materialised, then one rounding to fp16: otherwise the compiler may fold the
+          // last multiply and the conversion into one mixed-precision FMA in one inlined copy
+          // and not in another, and the same value would round differently by position
+          __asm__ volatile("" : "+v"(t));
+          v[e] = (half_t)t;
         }
         *reinterpret_cast<half4*>(&st[st_off(lane & 31, c4)]) = v;
       }

@@ -147,16 +147,7 @@ __global__ __launch_bounds__(NTT, 1) void transition_kernel(TransitionArgs p) {
   auto process = [&](int t, const half8 (&zq)[2]) {
     // 1. LayerNorm -> n_s
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = (float)zq[i][e];
-      ln_row128(v, g, bb, p.eps);
-      half8 o;
-#pragma unroll
-      for (int e = 0; e < 8; e++) o[e] = (half_t)v[e];
-      st16(&n_s[((tid >> 4) + 16 * i) * NSTR + ch0], o);
-    }
+    for (int i = 0; i < 2; i++) st16(&n_s[((tid >> 4) + 16 * i) * NSTR + ch0], ln_row128_h(zq[i], g, bb, p.eps));
     __syncthreads();
 
     // 2. D1[unit][cell] (and the gate branch), one chain per unit block

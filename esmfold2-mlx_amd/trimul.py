@@ -125,12 +125,16 @@ def prepare(pair_grid: torch.Tensor, visibility: torch.Tensor | None, C: int):
 
 
 class TriMulPair(nn.Module):
-    """z1 = z + T_out(z); z2 = z1 + T_in(z1) (mlx_trunk.py:93-95), residuals fused into kernel (c)."""
+    """z1 = z + T_out(z); z2 = z1 + T_in(z1) (mlx_trunk.py:93-95) in one ``tmu_pair_forward``:
+    at C = c = 128 five launches, the outgoing epilogue and the incoming projection fused
+    (z1 is written once and read back by the incoming epilogue only)."""
 
     def __init__(self, t_out: TriMul, t_in: TriMul):
         super().__init__()
         if not t_out.outgoing or t_in.outgoing:
             raise ValueError("TriMulPair takes an outgoing then an incoming update")
+        if (t_out.C, t_out.c) != (t_in.C, t_in.c):
+            raise ValueError(f"the two updates differ in width: {(t_out.C, t_out.c)} vs {(t_in.C, t_in.c)}")
         self.t_out, self.t_in = t_out, t_in
 
     def forward(self, z: torch.Tensor, mask: torch.Tensor | None = None, out: torch.Tensor | None = None):
@@ -138,7 +142,18 @@ class TriMulPair(nn.Module):
         if out is not None and (tuple(out.shape) != tuple(z16.shape) or out.dtype != F16 or not out.is_cuda
                                 or not out.is_contiguous()):
             raise capi.EsmError(-2, f"out must be a contiguous fp16 device tensor of shape {tuple(z16.shape)}")
-        z1 = torch.empty_like(z16) if out is None else out
-        self.t_out.run(z16, m16, z1, residual=True)
-        self.t_in.run(z1, m16, z1, residual=True)
-        return z1
+        return run_pair(self.t_out, self.t_in, z16, m16, torch.empty_like(z16) if out is None else out)
+
+
+def run_pair(o: TriMul, i: TriMul, z16: torch.Tensor, mask16: torch.Tensor | None, out: torch.Tensor) -> torch.Tensor:
+    """out = z1 + i(z1), z1 = z16 + o(z16) on the current stream (fp16; ``out`` may be ``z16``)."""
+    B, L = z16.shape[0], z16.shape[1]
+    base = o.workspace(B, L, z16.device).data_ptr()
+    capi.check(capi.lib().tmu_pair_forward(
+        z16.data_ptr(), None if mask16 is None else mask16.data_ptr(),
+        o.ln_in_w.data_ptr(), o.ln_in_b.data_ptr(), o.ln_in_eps, o.w_bundle.data_ptr(), o.ln_mix_w.data_ptr(),
+        o.ln_mix_b.data_ptr(), o.ln_mix_eps, o.w_emit.data_ptr(), o.w_gate.data_ptr(), int(o.out_mask),
+        i.ln_in_w.data_ptr(), i.ln_in_b.data_ptr(), i.ln_in_eps, i.w_bundle.data_ptr(), i.ln_mix_w.data_ptr(),
+        i.ln_mix_b.data_ptr(), i.ln_mix_eps, i.w_emit.data_ptr(), i.w_gate.data_ptr(), int(i.out_mask),
+        out.data_ptr(), base, B, L, o.C, o.c, capi.stream_ptr()))
+    return out

@@ -22,7 +22,7 @@ import torch
 from torch import nn
 
 from . import capi, kernels, scratch
-from .trimul import TriMul, prepare
+from .trimul import TriMul, prepare, run_pair
 
 F16 = torch.float16
 
@@ -93,8 +93,7 @@ class TrunkBlock(nn.Module):
 
     def run_(self, z16: torch.Tensor, m16: torch.Tensor | None) -> torch.Tensor:
         """In place on a contiguous fp16 [B, L, L, C] device tensor."""
-        self.tri_out.run(z16, m16, z16, residual=True)
-        self.tri_in.run(z16, m16, z16, residual=True)
+        run_pair(self.tri_out, self.tri_in, z16, m16, z16)
         return self.transition.run(z16, z16)
 
 

@@ -22,6 +22,6 @@ def test_counter_summary_has_every_tmu_kernel():
     import bench
 
     t = bench.measured_traffic()
-    for k in ("tmu_project_kernel", "tmu_contract_kernel", "tmu_epilogue_kernel"):
+    for k in ("tmu_project_kernel", "tmu_contract_frag_kernel", "tmu_epilogue_kernel"):
         # one TMU launch moves 43.5 MB algorithmically; the measured traffic stays within 15% of it
         assert 0.95 * 43.5e6 < t[k] < 1.15 * 43.5e6, (k, t.get(k))
