@@ -1,12 +1,11 @@
 """Benchmark: triangle multiplicative update pair cells/s at L=238, fp16, on one MI355X.
 
 A step is one TMU pair on the pair tensor z [1, 238, 238, 128] fp16:
-z1 = z + T_out(z), z2 = z1 + T_in(z1), inputs resident in HBM. value = L^2 / t_step
-(cells/s). The step makes the five launches TriMulPair / tmu_pair_forward make, through
-their single-launch entry points so that each can be timed on its own: T_out's projection
-(a) and contraction (b), the bridge (T_out's epilogue (c) fused with T_in's projection (a),
-z1 written once), T_in's contraction (b) and epilogue (c); a and b in the MFMA-fragment
-layout. It checks that their output equals TriMulPair's bit for bit.
+z1 = z + T_out(z), z2 = z1 + T_in(z1): six kernels (a, b, c per direction), inputs
+resident in HBM. value = L^2 / t_step (cells/s). The step makes the launches
+TriMulPair / tmu_forward make (a and b in the MFMA-fragment layout, through
+tmu_project_frag and tmu_contract_frag, so that each launch can be timed on its own),
+and checks that their output equals TriMulPair's bit for bit.
 
 Also reported on the same JSON line:
   roofline      for the kernel with the largest share of the step (achieved =
@@ -57,18 +56,13 @@ L, C, CL = 238, 128, 128
 
 
 def alg_counts(L: int, C: int, c: int):
-    """Algorithmic FLOPs and compulsory fp16 bytes per launch of each kernel, and its launches
-    per pair step."""
+    """Algorithmic FLOPs and compulsory fp16 bytes per launch of each kernel (one direction)."""
     N = L * L
-    k = {
-        "project": {"flops": 2 * N * C * 4 * c, "bytes": 2 * N * C + 2 * 2 * c * N, "per_step": 1},
-        "contract": {"flops": 2 * c * L ** 3, "bytes": 2 * 2 * c * N + 2 * c * N, "per_step": 2},
-        "epilogue": {"flops": 2 * N * (c * C + C * C), "bytes": 2 * c * N + 2 * N * C + 2 * N * C, "per_step": 1},
+    return {
+        "project": {"flops": 2 * N * C * 4 * c, "bytes": 2 * N * C + 2 * 2 * c * N},
+        "contract": {"flops": 2 * c * L ** 3, "bytes": 2 * 2 * c * N + 2 * c * N},
+        "epilogue": {"flops": 2 * N * (c * C + C * C), "bytes": 2 * c * N + 2 * N * C + 2 * N * C},
     }
-    # (c) then (a) without z1's round trip: reads x and z, writes z1, a and b
-    k["bridge"] = {"flops": k["epilogue"]["flops"] + k["project"]["flops"],
-                   "bytes": 2 * c * N + 2 * N * C + 2 * N * C + 2 * 2 * c * N, "per_step": 1}
-    return k
 
 
 PROFILE_COUNTERS = os.path.join(ROOT, "profiles", "bench_L238_counters.md")
@@ -240,33 +234,29 @@ def main():
     stream = torch.cuda.current_stream()
     scale = 1.0 / 256.0
 
-    def launch(kind):
+    def launch(kind, m: "pkg.trimul.TriMul", zin, zout):
         sp = pkg.capi.stream_ptr()  # the current stream: the capture stream while a graph records
-        o, i = t_out, t_in
-        if kind == "project":      # T_out (a) on z
-            rc = lib.tmu_project_frag(z0.data_ptr(), None, o.ln_in_w.data_ptr(), o.ln_in_b.data_ptr(), o.ln_in_eps,
-                                      o.w_bundle.data_ptr(), a.data_ptr(), b.data_ptr(), 1, L, C, CL, 0, sp)
+        if kind == "project":
+            rc = lib.tmu_project_frag(zin.data_ptr(), None, m.ln_in_w.data_ptr(), m.ln_in_b.data_ptr(), m.ln_in_eps,
+                                      m.w_bundle.data_ptr(), a.data_ptr(), b.data_ptr(), 1, L, C, CL,
+                                      int(not m.outgoing), sp)
         elif kind == "contract":
             rc = lib.tmu_contract_frag(a.data_ptr(), b.data_ptr(), x.data_ptr(), CL, L, ld, scale, sp)
-        elif kind == "bridge":     # T_out (c) into zbuf = z1, T_in (a) on z1
-            rc = lib.tmu_bridge(x.data_ptr(), ld, z0.data_ptr(), None, o.ln_in_w.data_ptr(), o.ln_in_b.data_ptr(),
-                                o.ln_in_eps, o.ln_mix_w.data_ptr(), o.ln_mix_b.data_ptr(), o.ln_mix_eps * scale * scale,
-                                o.w_emit.data_ptr(), o.w_gate.data_ptr(), 0, zbuf.data_ptr(), i.ln_in_w.data_ptr(),
-                                i.ln_in_b.data_ptr(), i.ln_in_eps, i.w_bundle.data_ptr(), a.data_ptr(), b.data_ptr(),
-                                1, L, C, CL, sp)
-        else:                      # T_in (c) in place on zbuf
-            rc = lib.tmu_epilogue(x.data_ptr(), ld, zbuf.data_ptr(), None, i.ln_in_w.data_ptr(), i.ln_in_b.data_ptr(),
-                                  i.ln_in_eps, i.ln_mix_w.data_ptr(), i.ln_mix_b.data_ptr(),
-                                  i.ln_mix_eps * scale * scale, i.w_emit.data_ptr(), i.w_gate.data_ptr(),
-                                  zbuf.data_ptr(), 1, L, C, CL, 1, 0, sp)
+        else:
+            rc = lib.tmu_epilogue(x.data_ptr(), ld, zin.data_ptr(), None, m.ln_in_w.data_ptr(), m.ln_in_b.data_ptr(),
+                                  m.ln_in_eps, m.ln_mix_w.data_ptr(), m.ln_mix_b.data_ptr(),
+                                  m.ln_mix_eps * scale * scale, m.w_emit.data_ptr(), m.w_gate.data_ptr(),
+                                  zout.data_ptr(), 1, L, C, CL, 1, 0, sp)
         pkg.capi.check(rc)
 
-    kinds = ("project", "contract", "bridge", "epilogue")
-    sequence = ("project", "contract", "bridge", "contract", "epilogue")
+    kinds = ("project", "contract", "epilogue")
 
     def step():
-        for kind in sequence:
-            launch(kind)
+        # z1 = z + T_out(z) written into zbuf; z2 = z1 + T_in(z1) in place
+        for d, m in enumerate((t_out, t_in)):
+            src = z0 if d == 0 else zbuf
+            for kind in kinds:
+                launch(kind, m, src, zbuf)
 
     # the benchmarked configuration's output, checked against the oracle in the CPU leg
     step()
@@ -274,7 +264,7 @@ def main():
     pair_out = zbuf.cpu()
     if not torch.isfinite(pair_out.float()).all():
         raise SystemExit("TMU pair output is not finite")
-    # the same launches as the module's own path (TriMulPair -> tmu_pair_forward): the same bits
+    # the same launches as the module's own path (TriMulPair -> tmu_forward): the same bits
     via_module = pkg.trimul.TriMulPair(t_out, t_in)(z0).cpu()
     if not torch.equal(via_module.view(torch.int16), pair_out.view(torch.int16)):
         raise SystemExit("the timed launches differ from TriMulPair's output")
@@ -315,12 +305,14 @@ def main():
     evs = []
     torch.cuda.synchronize()
     for _ in range(args.steps):
-        for k in sequence:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            launch(k)
-            e1.record(stream)
-            evs.append((k, e0, e1))
+        for d, m in enumerate((t_out, t_in)):
+            src = z0 if d == 0 else zbuf
+            for k in kinds:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                launch(k, m, src, zbuf)
+                e1.record(stream)
+                evs.append((k, e0, e1))
     torch.cuda.synchronize()
     for k, e0, e1 in evs:
         durs[k].append(e0.elapsed_time(e1) * 1e-3)
@@ -331,12 +323,10 @@ def main():
                    "mfma_frac": counts[k]["flops"] / t / MFMA_F16_PEAK,
                    "hbm_frac": counts[k]["bytes"] / t / HBM_PEAK}
     traffic = measured_traffic()
-    kname = {"project": "tmu_project_kernel", "contract": "tmu_contract_frag_kernel", "bridge": "tmu_bridge_kernel",
-             "epilogue": "tmu_epilogue_kernel"}
+    kname = {"project": "tmu_project_kernel", "contract": "tmu_contract_frag_kernel", "epilogue": "tmu_epilogue_kernel"}
     for k in kinds:
         kern[k]["traffic_bytes"] = traffic.get(kname[k])
-        kern[k]["launches_per_step"] = counts[k]["per_step"]
-    dom = max(kinds, key=lambda k: kern[k]["us"] * counts[k]["per_step"])  # the largest share of the step
+    dom = max(kinds, key=lambda k: kern[k]["us"])
     if dom == "contract":
         roof = {"bound": "mfma", "achieved": kern[dom]["tflops"], "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                 "frac": kern[dom]["mfma_frac"], "traffic": kern[dom]["traffic_bytes"], "kernel": kname[dom],
@@ -346,8 +336,8 @@ def main():
                 "frac": kern[dom]["hbm_frac"], "traffic": kern[dom]["traffic_bytes"], "kernel": kname[dom],
                 "per_launch": f"{counts[dom]['bytes'] / 1e6:.2f} MB"}
 
-    pair_flops = sum(counts[k]["flops"] for k in sequence)
-    pair_bytes = sum(counts[k]["bytes"] for k in sequence)
+    pair_flops = 2 * sum(v["flops"] for v in counts.values())
+    pair_bytes = 2 * sum(v["bytes"] for v in counts.values())
     out = {
         "metric": "tri-mul-update pair cells/sec at L=238 fp16 (+% MFMA peak, % HBM BW)",
         "value": L * L / (ms * 1e-3), "unit": "cells/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

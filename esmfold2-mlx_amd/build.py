@@ -21,7 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libesmfold2_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["project.hip", "contract.hip", "epilogue.hip", "bridge.hip", "q8.hip", "transition.hip", "esmc.hip",
+SOURCES = ["project.hip", "contract.hip", "epilogue.hip", "q8.hip", "transition.hip", "esmc.hip",
            "recycle.hip", "wide.hip", "capi.cpp"]
 HEADERS = ["common.h", "kernels.h", os.path.join("..", "..", "include", "esmfold2_amd.h")]
 ARCH = "gfx950"

@@ -35,8 +35,6 @@ SIGNATURES = {
     "tmu_pair_forward": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int,
                                 _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int,
                                 _vp, _vp, _int, _int, _int, _int, _vp]),
-    "tmu_bridge": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _f32, _vp, _vp, _int, _vp,
-                          _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "pair_transition": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "pair_transition_ws": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
     "pair_transition_workspace_bytes": (_sz, [_int, _int, _int, _int, _int]),

@@ -279,7 +279,6 @@ static int tmu_forward_wide(const esm_half* z, const esm_half* mask, const float
   if (esm::wide_gemm_blocks(g) > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_forward: too many tiles");
   e = esm::launch_wide_gemm(g, esm::kWideGateCM, st, cu_count());
   if (e != hipSuccess) return hip_status(e, "tmu_forward gate launch");
-  if (B * c > 65535) return fail(ESM_ERR_SHAPE, "tmu_forward: B=%d too large", B);
   esm::ContractArgs ca{wa, wb, wx, B * c, L, ld, ld, kScale, frag ? 1 : 0};
   e = esm::launch_contract(ca, st);
   if (e != hipSuccess) return hip_status(e, "tmu_forward contract launch");
@@ -316,24 +315,23 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
     return fail(ESM_ERR_UNSUPPORTED, "tmu_forward: C=%d c=%d (supported: C = c, 128 or a multiple of 128 up to 512)",
                 C, c);
   if (B == 0 || L == 0) return ok();
-  if (C != 128) {
-    if (!z || !ln_in_w || !ln_in_b || !w_bundle || !ln_mix_w || !ln_mix_b || !w_emit || !w_gate || !out)
-      return fail(ESM_ERR_NULL, "tmu_forward: NULL pointer");
-    if (!workspace) return fail(ESM_ERR_NULL, "tmu_forward: NULL workspace");
-    if (L > kMaxL) return fail(ESM_ERR_SHAPE, "tmu_forward: L=%d exceeds %d", L, kMaxL);
-    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
-      return fail(ESM_ERR_ALIGN, "tmu_forward: workspace must be 256-byte aligned");
-    if (!aligned16(z) || !aligned16(w_bundle) || !aligned16(w_emit) || !aligned16(w_gate) || !aligned16(out))
-      return fail(ESM_ERR_ALIGN, "tmu_forward: z, weights and out must be 16-byte aligned");
-    if (out == z && !residual) return fail(ESM_ERR_SHAPE, "tmu_forward: out may alias z only with residual=1");
-    if (out_mask && !mask) return fail(ESM_ERR_NULL, "tmu_forward: out_mask=1 needs a mask");
-    if (!(ln_in_eps >= 0.f) || !(ln_mix_eps >= 0.f)) return fail(ESM_ERR_SHAPE, "tmu_forward: eps must be >= 0");
-    return tmu_forward_wide(z, mask, ln_in_w, ln_in_b, ln_in_eps, w_bundle, ln_mix_w, ln_mix_b, ln_mix_eps, w_emit,
-                            w_gate, out, workspace, B, L, C, outgoing, residual, out_mask, stream);
-  }
+  // everything is checked here, before the first of the launches
+  if (!z || !ln_in_w || !ln_in_b || !w_bundle || !ln_mix_w || !ln_mix_b || !w_emit || !w_gate || !out)
+    return fail(ESM_ERR_NULL, "tmu_forward: NULL pointer");
   if (!workspace) return fail(ESM_ERR_NULL, "tmu_forward: NULL workspace");
+  if (L > kMaxL) return fail(ESM_ERR_SHAPE, "tmu_forward: L=%d exceeds %d", L, kMaxL);
+  if ((size_t)B * L * L * C >= (1ull << 30) || (long long)B * c > 65535)
+    return fail(ESM_ERR_SHAPE, "tmu_forward: B=%d L=%d C=%d: B*L*L*C must be < 2^30 and B*c <= 65535", B, L, C);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
     return fail(ESM_ERR_ALIGN, "tmu_forward: workspace must be 256-byte aligned");
+  if (!aligned16(z) || !aligned16(w_bundle) || !aligned16(w_emit) || !aligned16(w_gate) || !aligned16(out))
+    return fail(ESM_ERR_ALIGN, "tmu_forward: z, weights and out must be 16-byte aligned");
+  if (out == z && !residual) return fail(ESM_ERR_SHAPE, "tmu_forward: out may alias z only with residual=1");
+  if (out_mask && !mask) return fail(ESM_ERR_NULL, "tmu_forward: out_mask=1 needs a mask");
+  if (!(ln_in_eps >= 0.f) || !(ln_mix_eps >= 0.f)) return fail(ESM_ERR_SHAPE, "tmu_forward: eps must be >= 0");
+  if (C != 128)
+    return tmu_forward_wide(z, mask, ln_in_w, ln_in_b, ln_in_eps, w_bundle, ln_mix_w, ln_mix_b, ln_mix_eps, w_emit,
+                            w_gate, out, workspace, B, L, C, outgoing, residual, out_mask, stream);
   const int ld = tmu_leading_dim(L);
   const size_t plane = (size_t)B * c * tmu_plane_halfs(L);
   const size_t a256 = (plane * sizeof(esm_half) + 255) / 256 * 256 / sizeof(esm_half);
@@ -354,60 +352,6 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
                       w_emit, w_gate, out, B, L, C, c, residual, out_mask, stream);
 }
 
-int tmu_bridge(const esm_half* x, int ldx, const esm_half* z, const esm_half* mask, const float* o_ln_in_w,
-               const float* o_ln_in_b, float o_ln_in_eps, const float* o_ln_mix_w, const float* o_ln_mix_b,
-               float o_ln_mix_eps, const esm_half* o_w_emit, const esm_half* o_w_gate, int o_out_mask, esm_half* z1,
-               const float* i_ln_in_w, const float* i_ln_in_b, float i_ln_in_eps, const esm_half* i_w_bundle,
-               esm_half* a_out, esm_half* b_out, int B, int L, int C, int c, void* stream) {
-  if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_bridge: B=%d L=%d must be >= 0", B, L);
-  if (C != 128 || c != 128) return fail(ESM_ERR_UNSUPPORTED, "tmu_bridge: C=%d c=%d (supported: 128, 128)", C, c);
-  if (B == 0 || L == 0) return ok();
-  if (!x || !z || !o_ln_in_w || !o_ln_in_b || !o_ln_mix_w || !o_ln_mix_b || !o_w_emit || !o_w_gate || !z1 ||
-      !i_ln_in_w || !i_ln_in_b || !i_w_bundle || !a_out || !b_out)
-    return fail(ESM_ERR_NULL, "tmu_bridge: NULL pointer");
-  if (o_out_mask && !mask) return fail(ESM_ERR_NULL, "tmu_bridge: o_out_mask=1 needs a mask");
-  if (L > kMaxL) return fail(ESM_ERR_SHAPE, "tmu_bridge: L=%d exceeds %d", L, kMaxL);
-  if (ldx % 8 != 0 || ldx < L) return fail(ESM_ERR_SHAPE, "tmu_bridge: ldx=%d must be a multiple of 8, >= L", ldx);
-  if ((size_t)B * L * L * C * 2 >= (1ull << 31) || (size_t)B * c * L * ldx * 2 >= (1ull << 31))
-    return fail(ESM_ERR_SHAPE, "tmu_bridge: B=%d L=%d: z or x exceeds 2 GB", B, L);
-  if (!aligned16(x) || !aligned16(z) || !aligned16(o_w_emit) || !aligned16(o_w_gate) || !aligned16(z1) ||
-      !aligned16(i_w_bundle) || !aligned16(a_out) || !aligned16(b_out))
-    return fail(ESM_ERR_ALIGN, "tmu_bridge: x, z, z1, weights, a, b must be 16-byte aligned");
-  if (!(o_ln_in_eps >= 0.f) || !(o_ln_mix_eps >= 0.f) || !(i_ln_in_eps >= 0.f))
-    return fail(ESM_ERR_SHAPE, "tmu_bridge: eps must be >= 0");
-  esm::BridgeArgs g{};
-  g.x = H(x);
-  g.ldx = ldx;
-  g.z = H(z);
-  g.mask = mask ? H(mask) : nullptr;
-  g.lno_w = o_ln_in_w;
-  g.lno_b = o_ln_in_b;
-  g.lno_eps = o_ln_in_eps;
-  g.lnm_w = o_ln_mix_w;
-  g.lnm_b = o_ln_mix_b;
-  g.lnm_eps = o_ln_mix_eps;
-  g.w_emit = H(o_w_emit);
-  g.w_gate = H(o_w_gate);
-  g.out_mask = o_out_mask ? 1 : 0;
-  g.z1 = H(z1);
-  g.lni_w = i_ln_in_w;
-  g.lni_b = i_ln_in_b;
-  g.lni_eps = i_ln_in_eps;
-  g.w_bundle = H(i_w_bundle);
-  g.a = H(a_out);
-  g.b = H(b_out);
-  g.B = B;
-  g.L = L;
-  g.tpd = (L + 7) / 8;
-  g.rbn = (L + 31) / 32;
-  g.kbn = (L + 15) / 16;
-  const long long ntiles = (long long)B * g.tpd * g.tpd;
-  if (ntiles > 0x7fffffffLL) return fail(ESM_ERR_SHAPE, "tmu_bridge: too many tiles");
-  g.ntiles = (int)ntiles;
-  const int grid = (int)(ntiles < cu_count() ? ntiles : cu_count());
-  return hip_status(esm::launch_bridge(g, grid, (hipStream_t)stream), "tmu_bridge launch");
-}
-
 int tmu_pair_forward(const esm_half* z, const esm_half* mask, const float* o_ln_in_w, const float* o_ln_in_b,
                      float o_ln_in_eps, const esm_half* o_w_bundle, const float* o_ln_mix_w, const float* o_ln_mix_b,
                      float o_ln_mix_eps, const esm_half* o_w_emit, const esm_half* o_w_gate, int o_out_mask,
@@ -415,57 +359,23 @@ int tmu_pair_forward(const esm_half* z, const esm_half* mask, const float* o_ln_
                      const float* i_ln_mix_w, const float* i_ln_mix_b, float i_ln_mix_eps, const esm_half* i_w_emit,
                      const esm_half* i_w_gate, int i_out_mask, esm_half* out, void* workspace, int B, int L, int C,
                      int c, void* stream) {
+  // The incoming update's arguments are checked before the outgoing one launches: a bad
+  // argument launches nothing. (Its z is out, which the first call writes.)
   if (B < 0 || L < 0) return fail(ESM_ERR_SHAPE, "tmu_pair_forward: B=%d L=%d must be >= 0", B, L);
-  if (!((C == 128 && c == 128) || (C == c && wide_width(C))))
-    return fail(ESM_ERR_UNSUPPORTED,
-                "tmu_pair_forward: C=%d c=%d (supported: C = c, 128 or a multiple of 128 up to 512)", C, c);
-  if (B == 0 || L == 0) return ok();
-  if (C != 128) {  // two full updates, the second in place
-    int rc = tmu_forward(z, mask, o_ln_in_w, o_ln_in_b, o_ln_in_eps, o_w_bundle, o_ln_mix_w, o_ln_mix_b,
-                         o_ln_mix_eps, o_w_emit, o_w_gate, out, workspace, B, L, C, c, 1, 1, o_out_mask, stream);
-    if (rc) return rc;
-    return tmu_forward(out, mask, i_ln_in_w, i_ln_in_b, i_ln_in_eps, i_w_bundle, i_ln_mix_w, i_ln_mix_b,
-                       i_ln_mix_eps, i_w_emit, i_w_gate, out, workspace, B, L, C, c, 0, 1, i_out_mask, stream);
+  if (B > 0 && L > 0) {
+    if (!i_ln_in_w || !i_ln_in_b || !i_w_bundle || !i_ln_mix_w || !i_ln_mix_b || !i_w_emit || !i_w_gate)
+      return fail(ESM_ERR_NULL, "tmu_pair_forward: NULL pointer");
+    if (!aligned16(i_w_bundle) || !aligned16(i_w_emit) || !aligned16(i_w_gate))
+      return fail(ESM_ERR_ALIGN, "tmu_pair_forward: weights must be 16-byte aligned");
+    if (i_out_mask && !mask) return fail(ESM_ERR_NULL, "tmu_pair_forward: out_mask=1 needs a mask");
+    if (!(i_ln_in_eps >= 0.f) || !(i_ln_mix_eps >= 0.f))
+      return fail(ESM_ERR_SHAPE, "tmu_pair_forward: eps must be >= 0");
   }
-  // Everything is checked before the first launch, so a bad argument launches nothing.
-  if (!z || !o_ln_in_w || !o_ln_in_b || !o_w_bundle || !o_ln_mix_w || !o_ln_mix_b || !o_w_emit || !o_w_gate ||
-      !i_ln_in_w || !i_ln_in_b || !i_w_bundle || !i_ln_mix_w || !i_ln_mix_b || !i_w_emit || !i_w_gate || !out)
-    return fail(ESM_ERR_NULL, "tmu_pair_forward: NULL pointer");
-  if (!workspace) return fail(ESM_ERR_NULL, "tmu_pair_forward: NULL workspace");
-  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
-    return fail(ESM_ERR_ALIGN, "tmu_pair_forward: workspace must be 256-byte aligned");
-  if (L > kMaxL) return fail(ESM_ERR_SHAPE, "tmu_pair_forward: L=%d exceeds %d", L, kMaxL);
-  const int ld = tmu_leading_dim(L);
-  if ((size_t)B * L * L * C * 2 >= (1ull << 31) || (size_t)B * c * L * ld * 2 >= (1ull << 31))
-    return fail(ESM_ERR_SHAPE, "tmu_pair_forward: B=%d L=%d: z or x exceeds 2 GB", B, L);
-  if (B * c > 65535) return fail(ESM_ERR_SHAPE, "tmu_pair_forward: B=%d too large", B);
-  if (!aligned16(z) || !aligned16(o_w_bundle) || !aligned16(o_w_emit) || !aligned16(o_w_gate) ||
-      !aligned16(i_w_bundle) || !aligned16(i_w_emit) || !aligned16(i_w_gate) || !aligned16(out))
-    return fail(ESM_ERR_ALIGN, "tmu_pair_forward: z, weights and out must be 16-byte aligned");
-  if ((o_out_mask || i_out_mask) && !mask) return fail(ESM_ERR_NULL, "tmu_pair_forward: out_mask=1 needs a mask");
-  if (!(o_ln_in_eps >= 0.f) || !(o_ln_mix_eps >= 0.f) || !(i_ln_in_eps >= 0.f) || !(i_ln_mix_eps >= 0.f))
-    return fail(ESM_ERR_SHAPE, "tmu_pair_forward: eps must be >= 0");
-  const size_t plane = (size_t)B * c * tmu_plane_halfs(L);
-  const size_t a256 = (plane * sizeof(esm_half) + 255) / 256 * 256 / sizeof(esm_half);
-  esm_half* wa = static_cast<esm_half*>(workspace);
-  esm_half* wb = wa + a256;
-  esm_half* wx = wb + a256;
-  const float kScale = 1.0f / 256.0f;  // the contraction stored / 256, norm_mix's eps / 256^2
-  // outgoing (a), (b); the bridge: outgoing (c) into out and incoming (a) into the same a, b
-  // planes; incoming (b), (c) in place on out
-  int rc = project_impl(z, mask, o_ln_in_w, o_ln_in_b, o_ln_in_eps, o_w_bundle, wa, wb, B, L, C, c, ld, 0, true,
-                        stream);
+  int rc = tmu_forward(z, mask, o_ln_in_w, o_ln_in_b, o_ln_in_eps, o_w_bundle, o_ln_mix_w, o_ln_mix_b, o_ln_mix_eps,
+                       o_w_emit, o_w_gate, out, workspace, B, L, C, c, 1, 1, o_out_mask, stream);
   if (rc) return rc;
-  rc = tmu_contract_frag(wa, wb, wx, B * c, L, ld, kScale, stream);
-  if (rc) return rc;
-  rc = tmu_bridge(wx, ld, z, mask, o_ln_in_w, o_ln_in_b, o_ln_in_eps, o_ln_mix_w, o_ln_mix_b,
-                  o_ln_mix_eps * kScale * kScale, o_w_emit, o_w_gate, o_out_mask, out, i_ln_in_w, i_ln_in_b,
-                  i_ln_in_eps, i_w_bundle, wa, wb, B, L, C, c, stream);
-  if (rc) return rc;
-  rc = tmu_contract_frag(wa, wb, wx, B * c, L, ld, kScale, stream);
-  if (rc) return rc;
-  return tmu_epilogue(wx, ld, out, mask, i_ln_in_w, i_ln_in_b, i_ln_in_eps, i_ln_mix_w, i_ln_mix_b,
-                      i_ln_mix_eps * kScale * kScale, i_w_emit, i_w_gate, out, B, L, C, c, 1, i_out_mask, stream);
+  return tmu_forward(out, mask, i_ln_in_w, i_ln_in_b, i_ln_in_eps, i_w_bundle, i_ln_mix_w, i_ln_mix_b, i_ln_mix_eps,
+                     i_w_emit, i_w_gate, out, workspace, B, L, C, c, 0, 1, i_out_mask, stream);
 }
 
 // Checks shared by the q8 GEMM entry points (fn names the caller in the messages); out is

@@ -65,35 +65,6 @@ struct EpilogueArgs {
   int ntiles, tiles_per_line;
 };
 
-// The middle of a TMU pair at C = c = 128 (kernel (c) of the outgoing update fused with
-// kernel (a) of the incoming one): z1 = z + (LN_mix(x) W_e^T) * sigmoid(LN_in(z) W_g^T)
-// [* mask], then a', b' = the incoming projection of z1, in FragLayout planes.
-struct BridgeArgs {
-  const half_t* x;      // the outgoing contraction [B, c, L, ldx] (stored / 256)
-  int ldx;
-  const half_t* z;      // [B, L, L, C]
-  const half_t* mask;   // [B, L, L] or nullptr
-  const float* lno_w;   // outgoing norm_start [C]
-  const float* lno_b;
-  float lno_eps;
-  const float* lnm_w;   // outgoing norm_mix [c]
-  const float* lnm_b;
-  float lnm_eps;        // already divided by 256^2
-  const half_t* w_emit; // outgoing [C, c]
-  const half_t* w_gate; // outgoing [C, C]
-  int out_mask;         // multiply the outgoing update by the mask
-  half_t* z1;           // [B, L, L, C], may be z itself
-  const float* lni_w;   // incoming norm_start [C]
-  const float* lni_b;
-  float lni_eps;
-  const half_t* w_bundle;  // incoming [4c, C]
-  half_t* a;            // incoming operands, [B * c] FragLayout planes
-  half_t* b;
-  int B, L;
-  int tpd, ntiles;      // 8 x 8-cell tiles per dimension, in all
-  int rbn, kbn;
-};
-
 struct Q8Args {
   const half_t* x;      // [M, K]
   const uint8_t* q;     // [N, K]
@@ -227,7 +198,6 @@ constexpr int kEpiWaves = 8;
 hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s);
 hipError_t launch_contract(const ContractArgs& a, hipStream_t s);
 hipError_t launch_epilogue(const EpilogueArgs& a, int grid, hipStream_t s);
-hipError_t launch_bridge(const BridgeArgs& a, int grid, hipStream_t s);
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s);
 hipError_t launch_transition(const TransitionArgs& a, int grid, hipStream_t s);
 hipError_t launch_esmc_ln(const EsmcLnArgs& a, hipStream_t s);

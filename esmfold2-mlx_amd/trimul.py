@@ -125,9 +125,9 @@ def prepare(pair_grid: torch.Tensor, visibility: torch.Tensor | None, C: int):
 
 
 class TriMulPair(nn.Module):
-    """z1 = z + T_out(z); z2 = z1 + T_in(z1) (mlx_trunk.py:93-95) in one ``tmu_pair_forward``:
-    at C = c = 128 five launches, the outgoing epilogue and the incoming projection fused
-    (z1 is written once and read back by the incoming epilogue only)."""
+    """z1 = z + T_out(z); z2 = z1 + T_in(z1) (mlx_trunk.py:93-95) in one ``tmu_pair_forward``
+    call: the outgoing update with its residual fused into kernel (c), then the incoming one
+    in place."""
 
     def __init__(self, t_out: TriMul, t_in: TriMul):
         super().__init__()

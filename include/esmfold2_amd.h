@@ -178,7 +178,9 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
                 int c, int outgoing, int residual, int out_mask, void* stream);
 
 /*
- * The two triangle updates of a trunk block, out = z1 + T_in(z1), z1 = z + T_out(z).
+ * The two triangle updates of a trunk block, out = z1 + T_in(z1), z1 = z + T_out(z):
+ * tmu_forward for the outgoing update (residual, into out), then for the incoming one (in
+ * place on out), in one call.
  *
  * Replaces, in the reference:
  *   block_forward's first two lines                 mlx_trunk.py:94-95
@@ -187,10 +189,8 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
  *
  * o_* are the outgoing update's parameters and i_* the incoming update's, each as
  * tmu_forward takes them (o_out_mask / i_out_mask as its out_mask). out may be z itself.
- * workspace: tmu_workspace_bytes(B, L, c) bytes, 256-byte aligned.
- * At C = c = 128 this runs five launches: the outgoing (a) and (b), tmu_bridge (the
- * outgoing (c) fused with the incoming (a), z1 written once, to out), the incoming (b)
- * and (c) in place on out. Other widths: tmu_forward twice. Shape limits as tmu_forward.
+ * workspace: tmu_workspace_bytes(B, L, c) bytes, 256-byte aligned. Shape limits as
+ * tmu_forward; every argument is checked before the first launch.
  */
 int tmu_pair_forward(const esm_half* z, const esm_half* mask, const float* o_ln_in_w, const float* o_ln_in_b,
                      float o_ln_in_eps, const esm_half* o_w_bundle, const float* o_ln_mix_w, const float* o_ln_mix_b,
@@ -199,29 +199,6 @@ int tmu_pair_forward(const esm_half* z, const esm_half* mask, const float* o_ln_
                      const float* i_ln_mix_w, const float* i_ln_mix_b, float i_ln_mix_eps, const esm_half* i_w_emit,
                      const esm_half* i_w_gate, int i_out_mask, esm_half* out, void* workspace, int B, int L, int C,
                      int c, void* stream);
-
-/*
- * The middle launch of tmu_pair_forward at C = c = 128 (exposed so that a caller can run
- * or time it alone): the outgoing update's kernel (c) and the incoming update's kernel (a)
- * in one pass over the cells,
- *   z1 = z + (LN_mix(x) W_e^T) * sigmoid(LN_in(z) W_g^T) [* mask if o_out_mask]
- *   a_out, b_out = the incoming projection of z1 (as tmu_project_frag with incoming = 1).
- *
- * Replaces, in the reference: the outgoing _trimul's last two lines and the residual add
- * (mlx_trunk.py:89-90, :94), then the incoming _trimul's first three lines
- * (mlx_trunk.py:81-83) on the result.
- *
- * x            [B, c, L, ldx] the outgoing contraction as tmu_contract_frag stores it
- *              (scaled by 1/256: pass norm_mix's eps divided by 256^2).
- * z, mask      as tmu_forward; z1 [B, L, L, C] (may be z itself).
- * a_out, b_out [B * c] planes of the fragment layout (tmu_frag_plane_elems(L) each).
- * Supported: C = c = 128; ldx % 8 == 0, ldx >= L; pointers 16-byte aligned.
- */
-int tmu_bridge(const esm_half* x, int ldx, const esm_half* z, const esm_half* mask, const float* o_ln_in_w,
-               const float* o_ln_in_b, float o_ln_in_eps, const float* o_ln_mix_w, const float* o_ln_mix_b,
-               float o_ln_mix_eps, const esm_half* o_w_emit, const esm_half* o_w_gate, int o_out_mask, esm_half* z1,
-               const float* i_ln_in_w, const float* i_ln_in_b, float i_ln_in_eps, const esm_half* i_w_bundle,
-               esm_half* a_out, esm_half* b_out, int B, int L, int C, int c, void* stream);
 
 /*
  * Kernel (e): the pair transition, out = z + W3 act(W1 LN(z)) on every cell, with

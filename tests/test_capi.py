@@ -27,7 +27,7 @@ def test_header_declares_the_entry_points():
     for n in ("tmu_project", "tmu_contract", "tmu_epilogue", "tmu_forward", "q8_linear", "q8_linear_ws",
               "q8_linear_workspace_bytes", "q8_pack_scales", "q8_packed_scales_bytes",
               "pair_transition", "q8_dequant", "esm_last_error", "esm_version", "tmu_workspace_bytes", "tmu_leading_dim",
-              "tmu_pair_forward", "tmu_bridge"):
+              "tmu_pair_forward"):
         assert n in names
 
 
@@ -134,36 +134,27 @@ def test_rejects_null_and_bad_shapes(lib):
     assert lib.tmu_contract(odd, fake, fake, 1, 10, 16, 16, 1.0, None) == -3
 
 
-def test_pair_and_bridge_validate_before_launching(lib):
+def test_pair_forward_validates_before_launching(lib):
     f, ws = ctypes.c_void_p(4096), ctypes.c_void_p(1 << 20)
 
-    def pair(z=f, mask=None, workspace=ws, B=1, L=8, C=128, c=128, o_mask=0, i_mask=0, eps=1e-5, out=f):
+    def pair(z=f, mask=None, workspace=ws, B=1, L=8, C=128, c=128, o_mask=0, i_mask=0, eps=1e-5, out=f, i_w=f):
         o = [f, f, eps, f, f, f, eps, f, f, o_mask]
-        i = [f, f, eps, f, f, f, eps, f, f, i_mask]
+        i = [f, f, eps, i_w, f, f, eps, f, f, i_mask]
         return lib.tmu_pair_forward(z, mask, *o, *i, out, workspace, B, L, C, c, None)
 
-    def bridge(x=f, ldx=8, mask=None, B=1, L=8, C=128, c=128, o_mask=0, eps=1e-5, a=f):
-        return lib.tmu_bridge(x, ldx, f, mask, f, f, eps, f, f, eps, f, f, o_mask, f, f, f, eps, f, a, f, B, L, C, c,
-                              None)
-
     assert pair(C=192, c=192) == -4 and pair(C=256, c=128) == -4
-    assert pair(C=256, c=256, z=None) == -1        # the wide pair: two tmu_forward calls, checked there
+    assert pair(C=256, c=256, z=None) == -1
     assert pair(B=0) == 0 and pair(L=0) == 0
     assert pair(z=None) == -1 and pair(workspace=None) == -1
     assert pair(workspace=ctypes.c_void_p((1 << 20) + 16)) == -3
     assert pair(o_mask=1) == -1 and "mask" in _err(lib)
-    assert pair(i_mask=1) == -1
+    assert pair(i_mask=1) == -1                     # the incoming update's arguments: before any launch
+    assert pair(i_w=None) == -1 and pair(i_w=ctypes.c_void_p(4096 + 2)) == -3
     assert pair(eps=-1.0) == -2 and pair(eps=float("nan")) == -2
     assert pair(L=5000) == -2
     assert pair(z=ctypes.c_void_p(4096 + 2)) == -3
     assert pair(B=600) == -2                        # B * c beyond the contraction's grid
-    assert bridge(C=256, c=256) == -4
-    assert bridge(B=0) == 0
-    assert bridge(x=None) == -1
-    assert bridge(ldx=12) == -2 and bridge(ldx=0) == -2
-    assert bridge(o_mask=1) == -1
-    assert bridge(eps=-1.0) == -2
-    assert bridge(a=ctypes.c_void_p(4096 + 8)) == -3
+    assert pair(B=1, L=4000) == -2                  # B * L * L * C >= 2^30
 
 
 def test_library_matches_its_sources(pkg):
