@@ -165,6 +165,17 @@ DEV void dot2_moments(half4 v, float& s, float& q) {
     q = __builtin_amdgcn_fdot2(x, x, q, false);
   }
 }
+// gfx950's transposing LDS read, ds_read_b64_tr_b16: in each 16-lane group, lane j names the
+// 8-byte piece P_j (4 fp16 values) at p, and lane n receives P_{4e + n/4}[n % 4], e = 0..3.
+// With P_j = row r0 + j/4, columns c0 + 4 (j % 4) .. +3 of a row-major tile, lane n gets
+// column c0 + n of rows r0 .. r0+3.
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+DEV half4 ds_read_tr16x4(const void* p) {
+  const v4s_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s_t*)(__attribute__((address_space(3))) const char*)p);
+  return __builtin_bit_cast(half4, v);
+}
+
 // rstd = 1 / sqrt(var + eps) and shift = -mean * rstd from the sums over n values, with
 // var = E[x^2] - E[x]^2 in fp32 (clamped at 0). Against the two-pass form this loses about
 // n 2^-24 (1 + mean^2 / var) of var: below the fp16 rounding of the result while |mean| is

@@ -50,16 +50,12 @@ static_assert(U == 32, "a unit is one 32-column MFMA tile of cells");
 constexpr int RS = C + 8;
 DEV int cs_off(int cell, int k) { return cell * RS + 8 * k; }
 
-typedef short v4s __attribute__((ext_vector_type(4)));
 // ds_read_b64_tr_b16 of the x tile (channel-major, 64-byte rows of 32 cells): this lane
 // names the piece of 4 cells at (channel k0 + j/4, cells n0 + 4 (j % 4)), j = lane % 16;
 // it receives x[k0 + e][n0 + lane % 16] for e = 0..3.
 DEV half4 tr_read(const half_t* xs, int k0, int n0, int lane) {
   const int j = lane & 15;
-  const half_t* p = xs + (k0 + (j >> 2)) * U + n0 + 4 * (j & 3);
-  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4s*)(__attribute__((address_space(3))) half_t*)p);
-  return __builtin_bit_cast(half4, v);
+  return ds_read_tr16x4(xs + (k0 + (j >> 2)) * U + n0 + 4 * (j & 3));
 }
 
 // LayerNorm of one cell's 128 channels held as MFMA B-fragments: this lane holds channels

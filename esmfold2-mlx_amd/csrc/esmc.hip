@@ -211,16 +211,12 @@ __global__ __launch_bounds__(NTR) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
 // to consecutive bytes), with their 16-byte pieces XOR-swizzled: piece p of K row n at
 // p ^ ((n >> 1) & 7), so the fragment reads of 16 rows cover the 64 banks once; piece p of
 // V row n at p ^ (4 ((n >> 1) & 1)), so the 4 rows x 64 bytes of a transposing read pass do.
-typedef short v4s __attribute__((ext_vector_type(4)));
 // ds_read_b64_tr_b16 of V rows (128 bytes, pieces at p ^ (4 ((n >> 1) & 1))): lane j of a
 // 16-lane group names key row k0 + j / 4, d = n0 + 4 (j % 4) .. + 3; lane i receives
 // V[k0 + e][n0 + i % 16] for e = 0..3.
 DEV half4 tr_read_v(const char* vs, int k0, int n0, int lane) {
   const int j = lane & 15, n = k0 + (j >> 2), d = n0 + 4 * (j & 3);
-  const char* ptr = vs + n * 128 + 16 * ((d >> 3) ^ (((n >> 1) & 1) << 2)) + 2 * (d & 7);
-  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4s*)(__attribute__((address_space(3))) const char*)ptr);
-  return __builtin_bit_cast(half4, v);
+  return ds_read_tr16x4(vs + n * 128 + 16 * ((d >> 3) ^ (((n >> 1) & 1) << 2)) + 2 * (d & 7));
 }
 
 template <int NKB>

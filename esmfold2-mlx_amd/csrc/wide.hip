@@ -94,74 +94,99 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const void* __restrict__ x
 }
 
 // ---- LayerNorm over channels, channel-major -> cell-major -----------------------------------
-// One workgroup per 32 cells of one pair row: the c channel rows of 64 bytes are read with
-// coalesced 16-byte loads into LDS ([ch][cell], rows of 80 bytes); 8 threads per cell take the
-// channels g + 8 e (consecutive rows for neighbouring threads: distinct banks), fp32 two-pass
-// statistics over the 8 threads, and the normalised cell rows leave through LDS as whole
-// 16-byte pieces.
-constexpr int kCfCells = 32;
+// One 8-wave workgroup per 64 cells of one pair row. The c channel rows of 128 bytes arrive
+// as coalesced 16-byte loads into LDS ([ch][cell], rows of 160 bytes: the 8 rows one pass of
+// a transposing read touches cover the 64 banks once). Wave w takes the 16 cells
+// 16 (w % 4) + n and the channel half w / 4; ds_read_b64_tr_b16 gives lane (g, n) =
+// (lane / 16, lane % 16) the channels h c/2 + 4 g + 16 r .. +3 of its cell, so a lane holds
+// c/8 channels of one cell after c/32 reads. Statistics from v_dot2_f32_f16 (sums of x and
+// x^2) over the lane, the four lane groups (two exchanges) and the other channel half
+// (through LDS), var = E[x^2] - E[x]^2. The normalised values go back to LDS cell-major as
+// 8-byte pieces (4 channels) and leave as whole 16-byte pieces of the cell rows.
+constexpr int kCfCells = 64;
+constexpr int kCfThreads = 8 * kCfCells;  // two waves per 16 cells
 template <int CC>
-__global__ __launch_bounds__(256) void ln_cf_to_cl_kernel(const half_t* __restrict__ x, int ldx,
-                                                          const float* __restrict__ w, const float* __restrict__ b,
-                                                          float eps, half_t* __restrict__ y, int B, int L) {
-  constexpr int XS = kCfCells + 8;   // LDS row stride (halfs) of the channel-major tile
+__global__ __launch_bounds__(kCfThreads) void ln_cf_to_cl_kernel(const half_t* __restrict__ x, int ldx,
+                                                                 const float* __restrict__ w,
+                                                                 const float* __restrict__ b, float eps,
+                                                                 half_t* __restrict__ y, int B, int L) {
+  constexpr int XS = kCfCells + 16;  // LDS row stride (halfs) of the channel-major tile
   constexpr int YS = CC + 8;         // LDS row stride (halfs) of the cell-major tile
-  constexpr int PER = CC / 8;        // channels per thread
+  constexpr int NR = CC / 32;        // transposing reads per lane (4 channels each)
+  constexpr int NCB = kCfCells / 16; // 16-cell blocks
+  constexpr int NL = CC * (kCfCells / 8) / kCfThreads;  // 16-byte loads per thread
+  static_assert(CC % 64 == 0 && NL >= 1, "whole reads and loads per thread");
   __shared__ __align__(16) half_t xs[CC * XS];
   __shared__ __align__(16) half_t ys[kCfCells * YS];
-  const int tid = threadIdx.x;
+  __shared__ float st_s[2][kCfCells][2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int cb = wave % NCB, h = wave / NCB;
+  const int cell = 16 * cb + n;
+  const int ch0 = h * (CC / 2) + 4 * g;  // this lane's channels: ch0 + 16 r + e
+  float gw[NR][4], gb[NR][4];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      gw[r][e] = w[ch0 + 16 * r + e];
+      gb[r][e] = b[ch0 + 16 * r + e];
+    }
   const int tpl = (L + kCfCells - 1) / kCfCells;
   const long long ntiles = (long long)B * L * tpl;
   for (long long t = blockIdx.x; t < ntiles; t += gridDim.x) {
     const int bl = (int)(t / tpl);
     const int j0 = (int)(t - (long long)bl * tpl) * kCfCells;
     const int bi = bl / L, i = bl - bi * L;
-    // 1. c rows x 32 cells (4 pieces of 8 cells per row)
+    // 1. c rows x 64 cells (8 pieces of 8 cells per row)
     const rsrc_t rx = make_rsrc(x + ((size_t)bi * CC * L + i) * ldx + j0);
 #pragma unroll
-    for (int u = 0; u < CC * 4 / 256; u++) {
-      const int q = tid + 256 * u, row = q >> 2, part = q & 3;
+    for (int u = 0; u < NL; u++) {
+      const int q = tid + kCfThreads * u, row = q / (kCfCells / 8), part = q % (kCfCells / 8);
       const bool ok = j0 + 8 * part < ldx;
       st16(&xs[row * XS + 8 * part], bload16(rx, ok ? (uint32_t)((size_t)row * L * ldx + 8 * part) * 2u : kOOB));
     }
     __syncthreads();
-    // 2. statistics and normalisation: thread (cell, g), channels g + 8 e
-    const int cell = tid >> 3, gi = tid & 7;
-    float v[PER];
-    float s = 0.f;
+    // 2. this lane's channels of its cell (the lane names the piece of 4 cells at channel
+    //    ch0 + 16 r + n / 4, cells 16 cb + 4 (n % 4)); partial statistics, then the cell's
+    half4 v[NR];
+    float s = 0.f, q = 0.f;
 #pragma unroll
-    for (int e = 0; e < PER; e++) {
-      v[e] = (float)xs[(gi + 8 * e) * XS + cell];
-      s += v[e];
+    for (int r = 0; r < NR; r++) {
+      v[r] = ds_read_tr16x4(&xs[(ch0 + 16 * r + (n >> 2)) * XS + 16 * cb + 4 * (n & 3)]);
+      dot2_moments(v[r], s, q);
     }
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
-    const float mean = s * (1.0f / CC);
-    float qv = 0.f;
-#pragma unroll
-    for (int e = 0; e < PER; e++) {
-      v[e] -= mean;
-      qv += v[e] * v[e];
-    }
-    qv += __shfl_xor(qv, 1);
-    qv += __shfl_xor(qv, 2);
-    qv += __shfl_xor(qv, 4);
-    const float rstd = rsqrtf(qv * (1.0f / CC) + eps);
-#pragma unroll
-    for (int e = 0; e < PER; e++) {
-      const int ch = gi + 8 * e;
-      ys[cell * YS + ch] = (half_t)(v[e] * rstd * w[ch] + b[ch]);
+    s += __shfl_xor(s, 16);
+    q += __shfl_xor(q, 16);
+    s += __shfl_xor(s, 32);
+    q += __shfl_xor(q, 32);
+    if (g == 0) {
+      st_s[h][cell][0] = s;
+      st_s[h][cell][1] = q;
     }
     __syncthreads();
-    // 3. cell rows out: CC / 8 pieces of 16 bytes per cell
+    s += st_s[h ^ 1][cell][0];
+    q += st_s[h ^ 1][cell][1];
+    float rstd, shift;
+    ln_scale_shift(s, q, 1.0f / CC, eps, rstd, shift);
+    // 3. normalised pieces of 4 channels into the cell-major tile
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      half4 o;
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = ln_value(v[r][e], rstd, shift, gw[r][e], gb[r][e]);
+      *reinterpret_cast<half4*>(&ys[cell * YS + ch0 + 16 * r]) = o;
+    }
+    __syncthreads();
+    // 4. cell rows out: CC / 8 pieces of 16 bytes per cell
     half_t* yrow = y + ((size_t)bl * L + j0) * CC;
 #pragma unroll
-    for (int u = 0; u < kCfCells * (CC / 8) / 256; u++) {
-      const int q = tid + 256 * u, c2 = q / (CC / 8), piece = q - c2 * (CC / 8);
+    for (int u = 0; u < kCfCells * (CC / 8) / kCfThreads; u++) {
+      const int qq = tid + kCfThreads * u, c2 = qq / (CC / 8), piece = qq - c2 * (CC / 8);
       if (j0 + c2 < L) st16(yrow + (size_t)c2 * CC + 8 * piece, ld16(&ys[c2 * YS + 8 * piece]));
     }
-    __syncthreads();  // xs and ys are rewritten by the next tile
+    __syncthreads();  // xs, ys and the statistics are rewritten by the next tile
   }
 }
 
@@ -752,16 +777,16 @@ hipError_t launch_ln_cf_to_cl(const half_t* x, int ldx, const float* w, const fl
   const int grid = (int)(tiles < 16384 ? tiles : 16384);
   switch (c) {
     case 128:
-      hipLaunchKernelGGL((ln_cf_to_cl_kernel<128>), dim3(grid), dim3(256), 0, s, x, ldx, w, b, eps, y, B, L);
+      hipLaunchKernelGGL((ln_cf_to_cl_kernel<128>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
       break;
     case 256:
-      hipLaunchKernelGGL((ln_cf_to_cl_kernel<256>), dim3(grid), dim3(256), 0, s, x, ldx, w, b, eps, y, B, L);
+      hipLaunchKernelGGL((ln_cf_to_cl_kernel<256>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
       break;
     case 384:
-      hipLaunchKernelGGL((ln_cf_to_cl_kernel<384>), dim3(grid), dim3(256), 0, s, x, ldx, w, b, eps, y, B, L);
+      hipLaunchKernelGGL((ln_cf_to_cl_kernel<384>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
       break;
     case 512:
-      hipLaunchKernelGGL((ln_cf_to_cl_kernel<512>), dim3(grid), dim3(256), 0, s, x, ldx, w, b, eps, y, B, L);
+      hipLaunchKernelGGL((ln_cf_to_cl_kernel<512>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
       break;
     default:
       return hipErrorInvalidValue;
