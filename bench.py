@@ -31,7 +31,9 @@ Also reported on the same JSON line:
   pair_c256     the same TMU pair at ESMFold2's real width, C = c = 256 (the wide path);
   cpu_baseline  the CPU oracle (torch fp32 restatement of the reference's
                 _trimul_forward) on the host cores, a bounded sample of the same
-                workload (rank 0, N=1 only). This leg also verifies the GPU leg:
+                workload (rank 0, N=1 only), and each q8 linear's fp32
+                dequantise-then-matmul on the host (`q8_linear`, with the GPU's
+                speedup over it). This leg also verifies the GPU leg:
                 the benchmarked pair output and sampled q8 rows are compared with
                 the oracle's (the GPU leg itself imports nothing from oracle/).
 
@@ -136,7 +138,8 @@ def cpu_model() -> str:
 
 
 def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=None):
-    """The CPU oracle in fp32 on the host cores: 1 warm-up, median of 3 TMU pairs at L=238.
+    """The CPU oracle in fp32 on the host cores: 1 warm-up, median of 3 TMU pairs at L=238, and
+    the same for each benchmarked q8 linear (fp32 dequantisation and matmul, ``q8_linear``).
     It also verifies the GPU leg: the benchmarked pair output against the oracle's
     (max|err| / RMS(update), bar 1e-2) and the sampled q8 rows (normwise, bar 1e-3)."""
     import numpy as np
@@ -160,10 +163,20 @@ def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=Non
     upd_ref = ref.double() - z.double()
     upd_got = pair_out.double() - z.double()
     pair_err = float((upd_got - upd_ref).abs().max() / upd_ref.pow(2).mean().sqrt())
-    q8_err = {}
+    q8_err, q8_cpu = {}, {}
     for name, (rows, x, q, s, b, y) in q8_samples.items():
         yr = oq8.q8_linear(x[rows].numpy(), q.numpy(), s.numpy(), b.numpy())
         q8_err[name] = float(np.linalg.norm(y - yr) / np.linalg.norm(yr))
+        # the whole linear on the host: fp32 dequantisation, then the fp32 matmul
+        with torch.no_grad():
+            oq8.q8_linear_f32(x, q, s, b)
+            tq = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                oq8.q8_linear_f32(x, q, s, b)
+                tq.append(time.perf_counter() - t0)
+        q8_cpu[name] = {"ms": statistics.median(tq) * 1e3, "kind": "port",
+                        "sample": "fp32 dequantise then fp32 matmul (torch), median of 3 after 1 warm-up"}
     ok = pair_err <= 1e-2 and all(e <= 1e-3 for e in q8_err.values())
     stack_err = None
     if stack_case is not None:
@@ -202,6 +215,7 @@ def cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case=None, esmc_case=Non
             "cpu": cpu_model(), "host_cpus": os.cpu_count(), "torch_threads": threads,
             "sample": f"TMU pair (out+in, residuals) at L={L}, C=c={C}, fp32 torch on CPU, median of 3 after 1 "
                       f"warm-up, {t * 1e3:.1f} ms per pair",
+            "q8_linear": q8_cpu,
             "check": {"pair_max_err_over_rms": pair_err, "q8_rel_err_sample_rows": q8_err,
                       "block_stack_vs_oracle_fp64": stack_err, "esmc_block_max_err_over_rms": esmc_err,
                       "ok": ok}}
@@ -559,6 +573,9 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(z, po, pi, pair_out, q8_samples, stack_case, esmc_case)
         out["speedup_vs_cpu"] = out["value"] / out["cpu_baseline"]["value"]
+        for name, c in out["cpu_baseline"]["q8_linear"].items():
+            if name in out.get("q8", {}):
+                c["speedup_of_gpu"] = c["ms"] * 1e3 / out["q8"][name]["us"]
     print(json.dumps(out), flush=True)
     if not args.no_cpu and not out["cpu_baseline"]["check"]["ok"]:
         raise SystemExit("the benchmarked outputs differ from the oracle beyond the bars")

@@ -98,6 +98,15 @@ def dequant_f32(q, s, b, group: int = GROUP) -> np.ndarray:
     return dequant_exact(q, s, b, group).astype(np.float32)
 
 
+def q8_linear_f32(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, b: torch.Tensor,
+                  group: int = GROUP) -> torch.Tensor:
+    """The fp32 dequantise-then-matmul on the CPU (the CPU baseline's q8 linear): W_hat =
+    RN_fp32(s*q + b) in torch (s*q is exact in fp32, so the add is the one rounding: the bits of
+    ``dequant_f32``), then y = x @ W_hat^T with fp32 accumulation (mlx_esmc.py:78-81)."""
+    w = torch.repeat_interleave(s.float(), group, dim=1) * q.float() + torch.repeat_interleave(b.float(), group, dim=1)
+    return x.float() @ w.T
+
+
 def q8_linear(x: np.ndarray, q, s, b, group: int = GROUP, weights: str = "exact") -> np.ndarray:
     """y = x @ W_hat^T in fp64 (mlx_esmc.py:78-81). ``weights``: 'exact' or 'f16' (W_hat rounded to fp16)."""
     W = dequant_exact(q, s, b, group) if weights == "exact" else dequant_f16(q, s, b, group).astype(np.float64)

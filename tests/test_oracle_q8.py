@@ -153,3 +153,18 @@ def test_quantize_affine_properties():
     # fp16 casts of the parameters (the stored layer) stay within their own rounding
     q16, s16, b16 = q8.quantize_f16(w)
     assert np.array_equal(q16, q) and np.array_equal(s16, s.astype(np.float16))
+
+
+def test_linear_f32_is_dequant_f32_then_matmul():
+    # the CPU baseline's torch form: a one-hot x reads single weights, which must be
+    # dequant_f32's bits, and y stays within the fp32 error bound of the exact GEMM
+    import torch
+    x, q, s, b = q8.make_q8_inputs(5, 256, 48, seed=6)
+    tq, ts, tb = (torch.from_numpy(a) for a in (q, s, b))
+    wt = q8.q8_linear_f32(torch.eye(256, dtype=torch.float16), tq, ts, tb)
+    assert np.array_equal(wt.T.numpy(), q8.dequant_f32(q, s, b))
+    y = q8.q8_linear_f32(torch.from_numpy(x), tq, ts, tb).double().numpy()
+    ref = q8.q8_linear(x, q, s, b)
+    bound = 2 * (256 + 1) * 2.0 ** -24 * (np.abs(x.astype(np.float64)) @ np.abs(q8.dequant_exact(q, s, b)).T)
+    assert np.all(np.abs(y - ref) <= bound)
+    assert np.abs(y - ref).max() > 0  # fp32, not fp64
