@@ -97,6 +97,26 @@ def test_tmu_pair_256_full_size(gpu_lib, pkg):
     _bar(got, ref, z)
 
 
+def test_tmu_pair_256_L512_two_chain_padded(gpu_lib, pkg):
+    # the two-chain complex (300 + 160 residues, 52 padding positions) at the real width: tiles
+    # past the first 256 rows and columns, and the mask's zero rows and columns
+    L, C, valid = 512, 256, 460
+    z, mask, po, pi = tmu.make_pair_inputs(L, C, C, seed=4, dtype=torch.float16, pad_from=valid)
+    T = pkg.trimul
+    pair = T.TriMulPair(T.TriMul.from_weights(po), T.TriMul.from_weights(pi))
+    got = pair(z.to(DEV), mask.to(DEV)).double().cpu()
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    # beta_mix = 0 in this workload: padded cells receive an exactly-zero update (z unchanged)
+    v = torch.arange(L) >= valid
+    pad = v[:, None] | v[None, :]
+    assert torch.equal(got[0][pad], z[0][pad].double())
+    # the oracle in fp32 on the CPU (a few seconds here); the bar is 1e-2 * RMS of the update
+    with torch.no_grad():
+        ref = tmu.trimul_pair(z.float(), mask.float(), po, pi).double()
+    _bar(got, ref, z)
+
+
 @pytest.mark.parametrize("C,H,swiglu", [(256, 512, True), (256, 1024, True), (256, 1024, False), (128, 512, True),
                                         (384, 768, True), (256, 256, False), (256, 128, True), (512, 256, False)])
 def test_transition_wide_matches_oracle(gpu_lib, pkg, C, H, swiglu):
