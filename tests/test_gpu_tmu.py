@@ -236,6 +236,22 @@ def test_trimul_module(gpu_lib, pkg, L, outgoing, mask_kind):
     _bar(got, ref)
 
 
+@pytest.mark.parametrize("L", [8, 31, 33, 96, 160, 255, 257, 300])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_trimul_tile_edges(gpu_lib, pkg, L, outgoing):
+    # sizes either side of the tilings' edges: 8-cell and 16-k fragment tiles, 32-row MFMA blocks,
+    # 64-cell units and 128-row contraction blocks; random mask, random LN parameters, B = 1;
+    # the oracle in fp32 on the CPU (the larger sizes would take minutes in fp64)
+    p = _weights(11 * L + outgoing, outgoing, random_ln=True)
+    z, mask = _z(L + 1, 1, L), _mask(L + 2, 1, L, "random")
+    m = pkg.trimul.TriMul.from_weights(p)
+    got = m(z.to(DEV), mask.to(DEV))
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        ref = tmu.trimul(z.float(), mask.float(), p, outgoing)
+    _bar(got, ref)
+
+
 def test_trimul_fp32_plumbing_L76(gpu_lib, pkg):
     # config: outgoing only, z [1,76,76,128] fp32 N(0,1), seed 0, all-ones mask
     z, _, po, _ = tmu.make_pair_inputs(76, 128, 128, seed=0, dtype=torch.float32)

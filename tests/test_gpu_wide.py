@@ -65,6 +65,22 @@ def test_tmu_256_matches_oracle(gpu_lib, pkg, L, outgoing, mask_kind):
     _bar(upd, ref, torch.zeros_like(ref))
 
 
+@pytest.mark.parametrize("L", [8, 31, 129, 257])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_tmu_256_tile_edges(gpu_lib, pkg, L, outgoing):
+    # sizes either side of the wide path's tilings (8 x 8-cell fragment tiles, 64-cell line tiles,
+    # 128-row contraction blocks); random mask, random LN parameters; the oracle in fp32
+    C = 256
+    p = _weights(5 * L + outgoing, C, outgoing)
+    z = torch.randn(1, L, L, C, generator=torch.Generator().manual_seed(L + 9)).half()
+    m = _mask(L + 4, 1, L, "random")
+    mod = pkg.trimul.TriMul.from_weights(p)
+    upd = mod(z.to(DEV), m.to(DEV))
+    with torch.no_grad():
+        ref = tmu.trimul(z.float(), m.float(), p, outgoing)
+    _bar(upd, ref, torch.zeros_like(ref))
+
+
 @pytest.mark.parametrize("C,L,B", [(256, 40, 2), (384, 33, 1)])
 def test_tmu_wide_residual_out_mask_and_batch(gpu_lib, pkg, C, L, B):
     p = _weights(7, C, False)
