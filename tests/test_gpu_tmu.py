@@ -252,6 +252,30 @@ def test_trimul_tile_edges(gpu_lib, pkg, L, outgoing):
     _bar(got, ref)
 
 
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_trimul_permutation_equivariance_full_size(gpu_lib, pkg, outgoing):
+    # a size-independent property at the workload's size: relabelling the residues (the same
+    # permutation on i and j of z and of the mask) relabels the update, T(z_P) = T(z)_P. The two
+    # runs differ only in the contraction's summation order over k, which can flip a rounding of
+    # x: the oracle bar holds between them and most values are identical; a wrong index or a
+    # transposed operand in any kernel breaks both by O(1)
+    L = 238
+    p = _weights(91 + outgoing, outgoing, random_ln=True)
+    z, mask = _z(90, 1, L), _mask(92, 1, L, "random")
+    perm = torch.randperm(L, generator=torch.Generator().manual_seed(93))
+    zp = z[:, perm][:, :, perm].contiguous()
+    mp = mask[:, perm][:, :, perm].contiguous()
+    m = pkg.trimul.TriMul.from_weights(p)
+    got = m(z.to(DEV), mask.to(DEV)).double().cpu()
+    gotp = m(zp.to(DEV), mp.to(DEV)).double().cpu()
+    torch.cuda.synchronize()
+    expect = got[:, perm][:, :, perm]
+    _bar(gotp, expect)
+    same = float((gotp == expect).double().mean())
+    assert same > 0.9, f"only {same:.4f} of the values identical"
+    assert not torch.equal(gotp, got)  # the relabelling is not the identity
+
+
 def test_trimul_fp32_plumbing_L76(gpu_lib, pkg):
     # config: outgoing only, z [1,76,76,128] fp32 N(0,1), seed 0, all-ones mask
     z, _, po, _ = tmu.make_pair_inputs(76, 128, 128, seed=0, dtype=torch.float32)
