@@ -6,7 +6,11 @@
 // proj_gate (64 KB) are staged into LDS once and stay there; after that the waves never
 // synchronise: each wave owns whole units of 32 cells of one pair row i, cells
 // (i, pos0 .. pos0+31), taken in turn from a per-wave sequence (unit
-// 8 blockIdx.x + wave + 8 G k), so a CU's units spread over its four SIMDs.
+// 8 blockIdx.x + wave + 8 G k), so a CU's units spread over its four SIMDs. Waves 4-7
+// stage the weights while waves 0-3 issue their first unit's loads, and all meet at the
+// one barrier: the two waves of a SIMD then run their units a staging time apart, so one's
+// LayerNorms and GEMMs overlap the other's loads and stores (with every wave starting
+// together, each phase ran on all waves at once).
 //
 // Per unit, in a wave-private 8 KB LDS buffer:
 //   1. x[:, i, pos0:pos0+32] (128 channel rows of 64 contiguous bytes) and z's 32 cells
@@ -105,25 +109,26 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_epilogue_kernel(EpilogueArgs p
   const int h = lane >> 5, cell = lane & 31;
   constexpr bool use_mask = USE_MASK;  // out_mask with a mask: the update is multiplied by it
 
-  // Weights and LayerNorm parameters into LDS once (coalesced 16-byte rounds).
-  {
-    RowStage<C, NW * 64> re, rg;
-    re.load(p.w_emit, tid);
-    rg.load(p.w_gate, tid);
-    if (tid < C) {
-      lnp_s[0][tid] = p.ln_in_w[tid];
-      lnp_s[1][tid] = p.ln_in_b[tid];
-      lnp_s[2][tid] = p.ln_mix_w[tid];
-      lnp_s[3][tid] = p.ln_mix_b[tid];
+  // Weights and LayerNorm parameters into LDS once (coalesced 16-byte rounds), by waves 4-7.
+  constexpr int NST = (NW / 2) * 64;  // staging threads
+  auto stage_weights = [&]() {
+    const int ts = tid - NST;
+    RowStage<C, NST> re, rg;
+    re.load(p.w_emit, ts);
+    rg.load(p.w_gate, ts);
+    if (ts < C) {
+      lnp_s[0][ts] = p.ln_in_w[ts];
+      lnp_s[1][ts] = p.ln_in_b[ts];
+      lnp_s[2][ts] = p.ln_mix_w[ts];
+      lnp_s[3][ts] = p.ln_mix_b[ts];
     }
 #pragma unroll
-    for (int k = 0; k < RowStage<C, NW * 64>::kPer; k++) {
-      const int qq = tid + NW * 64 * k, r = qq >> 4, j = qq & 15;
+    for (int k = 0; k < RowStage<C, NST>::kPer; k++) {
+      const int qq = ts + NST * k, r = qq >> 4, j = qq & 15;
       st16(w_s + r * RS + 8 * j, re.v[k]);
       st16(w_s + (C + r) * RS + 8 * j, rg.v[k]);
     }
-    __syncthreads();
-  }
+  };
   const half_t* we_s = w_s;
   const half_t* wg_s = w_s + C * RS;
   half_t* bs = b_s[wave];
@@ -269,8 +274,25 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_epilogue_kernel(EpilogueArgs p
   // Consecutive units go to the waves of one workgroup: the two 32-cell halves of a
   // 128-byte line of x are then read on one CU (dealt to different XCDs, each half
   // fetched the whole line again: 1.8x the compulsory reads).
+  // Every wave passes the one barrier once: waves 0-3 with their first unit's loads in
+  // flight, waves 4-7 after the staging.
   const int G = gridDim.x;
-  for (int u = blockIdx.x * NW + wave; u < p.ntiles; u += G * NW) {
+  int u = blockIdx.x * NW + wave;
+  if (wave < NW / 2) {
+    UnitLoads ld;
+    load_unit(u, ld);
+    __syncthreads();
+    if (u < p.ntiles) process_unit(u, ld);
+  } else {
+    stage_weights();
+    __syncthreads();
+    if (u < p.ntiles) {
+      UnitLoads ld;
+      load_unit(u, ld);
+      process_unit(u, ld);
+    }
+  }
+  for (u += G * NW; u < p.ntiles; u += G * NW) {
     UnitLoads ld;
     load_unit(u, ld);
     process_unit(u, ld);
