@@ -77,9 +77,10 @@ class ParcaeLoop:
         self.exit_out = None  # on an early exit with source "coda": coda(readout(z)) of the exit step
 
     @classmethod
-    def from_model(cls, model, **kw) -> "ParcaeLoop":
+    def from_model(cls, model, coda=None, **kw) -> "ParcaeLoop":
         """From a 6B-shaped model: lm_encoder, folding_trunk and parcae_coda (FoldingTrunks or
-        PairTrunks), parcae_input_norm, parcae_readout, distogram_head, config.lm_encoder."""
+        PairTrunks), parcae_input_norm, parcae_readout, distogram_head, config.lm_encoder.
+        ``coda`` replaces ``model.parcae_coda`` (e.g. the module a wrapper holds)."""
         from .trunk import PairTrunk
         trunk = lambda m: m if isinstance(m, PairTrunk) else PairTrunk.from_folding_trunk(m)  # noqa: E731
         if abs(model.parcae_input_norm.eps - 1e-5) > 1e-12:
@@ -87,7 +88,8 @@ class ParcaeLoop:
         sig = DistogramSignal(model.distogram_head.weight, model.distogram_head.bias,
                               centers_6b() if model.distogram_head.weight.shape[0] == 64 else centers_experimental())
         return cls(trunk(model.lm_encoder), trunk(model.folding_trunk), model.parcae_input_norm.weight,
-                   model.parcae_input_norm.bias, model.parcae_readout.weight, sig, coda=trunk(model.parcae_coda),
+                   model.parcae_input_norm.bias, model.parcae_readout.weight, sig,
+                   coda=trunk(model.parcae_coda if coda is None else coda),
                    lm_dropout=model.config.lm_encoder.lm_dropout, **kw)
 
     def step(self, z, z_init, lm_z_i, a, b16, mask=None):

@@ -27,6 +27,14 @@ from .trimul import TriMul, prepare, run_pair
 F16 = torch.float16
 
 
+def relay_trunk_setting(inner, name: str, value) -> None:
+    """Pass a FoldingTrunk setting (``set_chunk_size``, ``set_kernel_backend``) from a wrapper to
+    the module it wraps, when that module takes it; the HIP kernels need neither."""
+    setter = getattr(inner, name, None)
+    if callable(setter):
+        setter(value)
+
+
 class PairTransition(nn.Module):
     """z + W3 act(W1 LN(z)): ReLU MLP (w2 None) or the reference's SwiGLU (fast_trunk.py:35-42)."""
 

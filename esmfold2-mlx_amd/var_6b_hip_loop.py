@@ -1,105 +1,132 @@
 """Variant (6B release model): the parcae recycling loop on the HIP kernels, with an optional
-early exit once the predicted distances stop changing (the reference's var_6b_mlx_loop,
-var_6b_mlx_loop.py:1-35, :116-236).
+early exit (the reference's var_6b_mlx_loop; behaviour of var_6b_mlx_loop.py:157-207, plugin
+contract of :225-236).
 
-``apply(model)`` installs ``model._run_one_loop`` as an instance attribute (upstream's
-forward calls it by name, var_6b_mlx_loop.py:231) with upstream's signature
-``(z, z_init, lm_z, msa_inputs, pair_mask, a, b_mat, tok_mask, total_steps)``. Per step the
-dropout stays in PyTorch (upstream's draws in upstream's order); the LM encoder, the parcae
-recurrence and the trunk run on the HIP kernels (``recycle.ParcaeLoop`` over ``PairTrunk``s:
-stacks already swapped by ``var_6b_hip_trunks`` are used as they are, others are converted).
+What ``apply(model, **policy)`` installs:
 
-Early exit (``adaptive=True``): after step k >= min_steps and before the last, the 95th
-percentile of |change| of the distogram's expected distance (source "coda": readout ->
-coda -> head, the real output path; "readout": readout -> head) below ``threshold`` returns z.
-With source "coda" the exit step's coda output is handed on to forward: ``parcae_readout``
-and ``parcae_coda`` are wrapped so that forward's readout of the returned z gives that output
-and the coda passes it through (var_6b_mlx_loop.py:88-113, :232-234). ``burn_rng`` draws the
-skipped steps' dropout masks so later random draws match the full-length fold.
+* ``model._run_one_loop`` -- the name upstream's forward calls, with upstream's arguments
+  ``(z, z_init, lm_z, msa_inputs, pair_mask, a, b_mat, tok_mask, total_steps)`` -- bound to a
+  ``HipLoop``, which runs ``recycle.ParcaeLoop`` over ``PairTrunk`` stacks (stacks that
+  ``var_6b_hip_trunks`` already swapped are used as they are). The dropout is drawn by torch in
+  upstream's order; the LM encoder, the recurrence and the trunk are HIP kernels.
+* With an exit on the coda path (``ExitPolicy.adaptive`` and ``source == "coda"``) the loop has
+  already computed ``coda(readout(z))`` for the step it stops at. One ``ExitHandoff`` object owns
+  that result until forward consumes it: a forward hook on ``parcae_readout`` swaps the readout
+  of the returned ``z`` for the stored coda output, and ``parcae_coda`` is an ``ExitCache`` that
+  passes that tensor through instead of running the coda again. Any other input takes the
+  ordinary path, and the hand-off is dropped once used.
 """
 
 from __future__ import annotations
 
+import dataclasses
+from dataclasses import dataclass
+
+import torch
 from torch import nn
 
 from .recycle import ParcaeLoop
+from .trunk import relay_trunk_setting
 
-# Early-exit policy (off here; var_6b_hip_adaptive sets it), var_6b_mlx_loop.py:46-54.
-SOURCE = "coda"
-THRESHOLD = None
-MIN_STEPS = 2
-BURN_RNG = True
+SOURCES = ("coda", "readout")
+
+
+@dataclass(frozen=True)
+class ExitPolicy:
+    """When the loop may stop early. ``adaptive=False`` runs every scheduled step. Otherwise,
+    after step k >= ``min_steps`` and before the last, the loop stops once the 95th percentile of
+    the change of the distogram's expected distance (on ``source``: "coda" = readout -> coda ->
+    head, the path forward takes; "readout" = readout -> head) is below ``threshold`` (A).
+    ``burn_rng`` still draws the skipped steps' dropout masks, so later random draws match the
+    full-length fold (var_6b_mlx_loop.py:46-50)."""
+
+    adaptive: bool = False
+    threshold: float | None = None
+    source: str = "coda"
+    min_steps: int = 2
+    burn_rng: bool = True
+
+    def __post_init__(self):
+        if self.source not in SOURCES:
+            raise ValueError(f"source {self.source!r}: one of {SOURCES}")
+        if self.adaptive and self.threshold is None:
+            raise ValueError("an adaptive loop needs a threshold")
+
+    @property
+    def hands_off_coda(self) -> bool:
+        return self.adaptive and self.source == "coda"
+
+
+class ExitHandoff:
+    """The exit step's ``(z, coda output)`` pair, held from the loop's return until forward's
+    readout -> coda sequence has consumed it (one use)."""
+
+    def __init__(self):
+        self.z = self.out = None
+
+    def arm(self, z: torch.Tensor, out: torch.Tensor) -> None:
+        self.z, self.out = z, out
+
+    def clear(self) -> None:
+        self.z = self.out = None
+
+    def readout_hook(self, module, args, output):
+        """Forward hook of ``parcae_readout``: the readout of the exit ``z`` becomes the coda
+        output the loop already computed (returning None keeps the module's own output)."""
+        if self.z is not None and args and args[0] is self.z:
+            return self.out
+        return None
+
+    def pass_through(self, x) -> torch.Tensor | None:
+        """For the coda: ``x`` itself if it is the stored output (and the hand-off ends), else None."""
+        if self.out is not None and x is self.out:
+            self.clear()
+            return x
+        return None
 
 
 class ExitCache(nn.Module):
-    """A stand-in for ``parcae_readout`` or ``parcae_coda`` that reuses the loop's exit-step
-    coda output: readout(z_exit) returns it, and the coda returns that same tensor unchanged
-    (clearing the cache); any other input goes to the wrapped module."""
+    """``parcae_coda`` under an exit hand-off: the stored coda output passes straight through;
+    every other input runs the wrapped coda (``inner``)."""
 
-    def __init__(self, inner: nn.Module, loop: "HipLoop", role: str):
+    def __init__(self, inner: nn.Module, handoff: ExitHandoff):
         super().__init__()
-        if role not in ("readout", "coda"):
-            raise ValueError("role is 'readout' or 'coda'")
         self.inner = inner
-        self.__dict__["_loop"] = loop  # not a submodule: the model's state dict is unchanged
-        self.role = role
+        self.__dict__["handoff"] = handoff  # plain attribute: the state dict keeps the coda's keys only
 
     def set_chunk_size(self, chunk_size):
-        if hasattr(self.inner, "set_chunk_size"):
-            self.inner.set_chunk_size(chunk_size)
+        relay_trunk_setting(self.inner, "set_chunk_size", chunk_size)
 
     def set_kernel_backend(self, backend):
-        if hasattr(self.inner, "set_kernel_backend"):
-            self.inner.set_kernel_backend(backend)
+        relay_trunk_setting(self.inner, "set_kernel_backend", backend)
 
-    def forward(self, x, *a, **k):
-        loop = self._loop
-        if self.role == "readout" and loop.exit_z is not None and x is loop.exit_z:
-            return loop.exit_out
-        if self.role == "coda" and loop.exit_out is not None and x is loop.exit_out:
-            loop.exit_z = loop.exit_out = None
-            return x
-        return self.inner(x, *a, **k)
+    def forward(self, x, *args, **kwargs):
+        done = self.handoff.pass_through(x)
+        return self.inner(x, *args, **kwargs) if done is None else done
 
 
-def _unwrapped(m):
-    return m.inner if isinstance(m, ExitCache) else m
+def _bare_coda(model) -> nn.Module:
+    coda = model.parcae_coda
+    return coda.inner if isinstance(coda, ExitCache) else coda
 
 
 class HipLoop:
-    """The loop object ``apply`` installs: ``run`` is upstream's ``_run_one_loop``."""
+    """The installed loop: ``run`` has upstream's ``_run_one_loop`` signature."""
 
-    def __init__(self, model, adaptive: bool = False, threshold=None, source=None, min_steps=None, burn_rng=None):
-        self.model = model
-        self.adaptive = bool(adaptive)
-        self.threshold = THRESHOLD if threshold is None else threshold
-        self.source = source or SOURCE
-        self.min_steps = MIN_STEPS if min_steps is None else min_steps
-        self.burn_rng = BURN_RNG if burn_rng is None else burn_rng
-        if self.adaptive and self.threshold is None:
-            raise ValueError("adaptive recycling needs a threshold")
+    def __init__(self, model, policy: ExitPolicy = ExitPolicy()):
+        self.model, self.policy = model, policy
+        self.handoff = ExitHandoff()
+        self.loop = ParcaeLoop.from_model(
+            model, coda=_bare_coda(model), threshold=policy.threshold if policy.adaptive else None,
+            source=policy.source, min_steps=policy.min_steps, burn_rng=policy.burn_rng)
 
-        class _View:  # the model with its readout / coda unwrapped, for ParcaeLoop.from_model
-            pass
+    # what a caller inspects after a fold
+    steps_run = property(lambda self: self.loop.steps_run)
+    history = property(lambda self: self.loop.history)
+    exit_z = property(lambda self: self.handoff.z)
+    exit_out = property(lambda self: self.handoff.out)
 
-        view = _View()
-        for name in ("lm_encoder", "folding_trunk", "parcae_input_norm", "distogram_head", "config"):
-            setattr(view, name, getattr(model, name))
-        view.parcae_readout = _unwrapped(model.parcae_readout)
-        view.parcae_coda = _unwrapped(model.parcae_coda)
-        self.loop = ParcaeLoop.from_model(view, threshold=self.threshold if self.adaptive else None,
-                                          source=self.source, min_steps=self.min_steps, burn_rng=self.burn_rng)
-        self.exit_z = self.exit_out = None
-
-    @property
-    def steps_run(self) -> int:
-        return self.loop.steps_run
-
-    @property
-    def history(self):
-        return self.loop.history
-
-    def run(self, z, z_init, lm_z, msa_inputs, pair_mask, a, b_mat, tok_mask, total_steps):
+    def _check_inputs(self, msa_inputs, lm_z):
         m = self.model
         if msa_inputs is not None or getattr(m, "msa_encoder", None) is not None:
             raise NotImplementedError("MSA input is not supported (var_6b_mlx_loop.py:159)")
@@ -107,21 +134,41 @@ class HipLoop:
             raise ValueError("the parcae loop needs lm_z and an lm_encoder")
         if not getattr(m.config.lm_encoder, "per_loop_lm_dropout", False):
             raise ValueError("the loop draws a fresh LM dropout per step (config.lm_encoder.per_loop_lm_dropout)")
-        self.exit_z = self.exit_out = None
+
+    def run(self, z, z_init, lm_z, msa_inputs, pair_mask, a, b_mat, tok_mask, total_steps):
+        self._check_inputs(msa_inputs, lm_z)
+        self.handoff.clear()
         z_out = self.loop.run(z, z_init, lm_z, pair_mask, a, b_mat, total_steps)
-        if self.loop.exit_out is not None:  # forward's readout -> coda will return this
-            self.exit_z, self.exit_out = z_out, self.loop.exit_out
+        if self.loop.exit_out is not None and self.policy.hands_off_coda:
+            self.handoff.arm(z_out, self.loop.exit_out)
         return z_out
 
 
-def apply(model, **kw) -> HipLoop:
-    loop = HipLoop(model, **kw)
-    model._run_one_loop = loop.run  # instance attribute: forward's self._run_one_loop(...) finds it
-    if loop.adaptive and loop.source == "coda" and not isinstance(model.parcae_readout, ExitCache):
-        model.parcae_readout = ExitCache(model.parcae_readout, loop, "readout")
-        model.parcae_coda = ExitCache(model.parcae_coda, loop, "coda")
-    elif isinstance(model.parcae_readout, ExitCache):  # re-applied: point the caches at this loop
-        model.parcae_readout.__dict__["_loop"] = loop
-        model.parcae_coda.__dict__["_loop"] = loop
+def _install_handoff(model, loop: HipLoop) -> None:
+    """Wrap the coda once and point it, and a single readout hook, at this loop's hand-off."""
+    if not isinstance(model.parcae_coda, ExitCache):
+        model.parcae_coda = ExitCache(model.parcae_coda, loop.handoff)
+    else:
+        model.parcae_coda.__dict__["handoff"] = loop.handoff
+    old = model.__dict__.get("_hip_readout_hook")
+    if old is not None:
+        old.remove()
+    model.__dict__["_hip_readout_hook"] = model.parcae_readout.register_forward_hook(loop.handoff.readout_hook)
+
+
+def install(model, policy: ExitPolicy) -> HipLoop:
+    loop = HipLoop(model, policy)
+    model._run_one_loop = loop.run  # the instance attribute shadows the class's method
+    if policy.hands_off_coda or isinstance(model.parcae_coda, ExitCache):
+        _install_handoff(model, loop)  # a re-install also retargets an earlier wrapper
     model._hip_loop = loop
     return loop
+
+
+def apply(model, **policy) -> HipLoop:
+    """Install the loop with ``ExitPolicy(**policy)`` (no early exit by default)."""
+    return install(model, ExitPolicy(**policy))
+
+
+def with_policy(base: ExitPolicy, **overrides) -> ExitPolicy:
+    return dataclasses.replace(base, **overrides)
