@@ -10,11 +10,14 @@ output is checked to equal TriMulPair's bit for bit.
 
 Also reported on the same JSON line:
   roofline      for the kernel with the largest share of the step (achieved =
-                algorithmic bytes or flops per launch / its mean duration, measured
-                with HIP events on the launch stream around its launches in a
-                second pass of real steps; traffic = calibrated rocprofv3
+                algorithmic bytes or flops per launch / its mean duration over a
+                second pass of the timed step, from start/stop events the runtime
+                stamps with each kernel's own begin and end (the durations a
+                kernel trace reports); traffic = calibrated rocprofv3
                 FETCH_SIZE + WRITE_SIZE per launch from profiles/);
-  kernels       the same figures for every kernel of the step;
+  kernels       the same figures for every kernel of the step, and for the
+                contraction its fraction of its own roof, min(MFMA peak, AI x HBM
+                peak) with AI = L/3 FLOP/B by compulsory traffic;
   q8            the 8-bit ESMC-style linears [238,2560]x[2560->10240] and
                 [238,10240]x[10240->2560] (time, TFLOP/s, GB/s);
   transition    the pair transition kernel (LN -> 128->512 -> ReLU -> 512->128 + z)
@@ -303,6 +306,7 @@ def main():
         torch.cuda.synchronize()
 
     # timed region: exactly `steps` steps between synchronisations
+    kname = {"project": "tmu_project_kernel", "contract": "tmu_contract_frag_kernel", "epilogue": "tmu_epilogue_kernel"}
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -316,35 +320,43 @@ def main():
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
 
-    # per-kernel durations: HIP events around every launch over a second pass of real steps
-    # (the kernels see the pipeline's cache state; each event pair adds ~1 us of dispatch,
-    # so the figures err slow against rocprofv3's). Launching one kernel back to back
-    # instead keeps its inputs in the 256 MB last-level cache and reads 10-15% fast.
+    # per-kernel durations: a second pass of the same eager steps (TriMulPair, one
+    # tmu_pair_forward call each) whose six launches carry start/stop events that the runtime
+    # stamps with each kernel's own begin and end (capi.KernelTimes, hipExtLaunchKernelGGL), i.e.
+    # the durations a profiler's kernel trace reports. Not inside the timed region: a launch that
+    # carries the events costs ~7 us more of dispatch (the step went from 91 to 133 us), though
+    # the kernel's own duration does not change. The events are created before the pass.
+    nk = 6 * args.steps
+    with pkg.capi.KernelTimes(nk):
+        pass
+    kt = pkg.capi.KernelTimes(nk)
+    torch.cuda.synchronize()
+    with kt:
+        for _ in range(args.steps):
+            step()
+    torch.cuda.synchronize()
+    per_name = kt.by_kernel()
+
     counts = alg_counts(L, C, CL)
     kern = {}
-    durs = {k: [] for k in kinds}
-    evs = []
-    torch.cuda.synchronize()
-    for _ in range(args.steps):
-        for d, m in enumerate((t_out, t_in)):
-            src = z0 if d == 0 else zbuf
-            for k in kinds:
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                launch(k, m, src, zbuf)
-                e1.record(stream)
-                evs.append((k, e0, e1))
-    torch.cuda.synchronize()
-    for k, e0, e1 in evs:
-        durs[k].append(e0.elapsed_time(e1) * 1e-3)
     for k in kinds:
-        t = statistics.median(durs[k])  # robust to a stray slow event pair
-        kern[k] = {"us": t * 1e6, "tflops": counts[k]["flops"] / t / 1e12,
+        ts = [t for name, v in per_name.items() if name.startswith(kname[k]) for t in v]
+        if len(ts) != 2 * args.steps:
+            raise SystemExit(f"expected {2 * args.steps} timed launches of {kname[k]}, got {len(ts)}")
+        t = statistics.fmean(ts) * 1e-6  # the mean, as rocprofv3 --stats reports it
+        kern[k] = {"us": t * 1e6, "us_median": statistics.median(ts), "launches": len(ts),
+                   "tflops": counts[k]["flops"] / t / 1e12,
                    "gbs": counts[k]["bytes"] / t / 1e9,
                    "mfma_frac": counts[k]["flops"] / t / MFMA_F16_PEAK,
                    "hbm_frac": counts[k]["bytes"] / t / HBM_PEAK}
+    # the contraction's own roof: by its compulsory traffic (AI = flops / bytes = L/3) it cannot
+    # beat AI x HBM peak, far below the MFMA peak at this L
+    ai = counts["contract"]["flops"] / counts["contract"]["bytes"]
+    cap = min(MFMA_F16_PEAK, ai * HBM_PEAK)
+    kern["contract"].update({"ai_flop_per_byte": ai, "cap_tflops": cap / 1e12,
+                             "cap_bound": "hbm" if cap < MFMA_F16_PEAK else "mfma",
+                             "cap_frac": counts["contract"]["flops"] / (kern["contract"]["us"] * 1e-6) / cap})
     traffic = measured_traffic()
-    kname = {"project": "tmu_project_kernel", "contract": "tmu_contract_frag_kernel", "epilogue": "tmu_epilogue_kernel"}
     for k in kinds:
         kern[k]["traffic_bytes"] = traffic.get(kname[k])
     dom = max(kinds, key=lambda k: kern[k]["us"])
@@ -356,6 +368,8 @@ def main():
         roof = {"bound": "hbm", "achieved": kern[dom]["gbs"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": kern[dom]["hbm_frac"], "traffic": kern[dom]["traffic_bytes"], "kernel": kname[dom],
                 "per_launch": f"{counts[dom]['bytes'] / 1e6:.2f} MB"}
+    roof["duration"] = (f"mean of {kern[dom]['launches']} runtime-stamped kernel durations (hipExtLaunchKernelGGL "
+                        "events) over a second pass of the timed step")
 
     pair_flops = 2 * sum(v["flops"] for v in counts.values())
     pair_bytes = 2 * sum(v["bytes"] for v in counts.values())

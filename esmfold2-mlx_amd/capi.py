@@ -21,6 +21,9 @@ SIGNATURES = {
     "esm_last_error": (ctypes.c_char_p, []),
     "esm_version": (ctypes.c_char_p, []),
     "esm_source_hash": (ctypes.c_char_p, []),
+    "esm_timing_begin": (_int, [_int]),
+    "esm_timing_end": (_int, [_vp, _int, _vp]),
+    "esm_timing_name": (ctypes.c_char_p, [_int]),
     "tmu_workspace_bytes": (_sz, [_int, _int, _int]),
     "tmu_leading_dim": (_int, [_int]),
     "tmu_project": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp]),
@@ -35,6 +38,11 @@ SIGNATURES = {
     "tmu_pair_forward": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int,
                                 _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int,
                                 _vp, _vp, _int, _int, _int, _int, _vp]),
+    "tmu_forward_ws": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _sz, _int, _int,
+                              _int, _int, _int, _int, _int, _vp]),
+    "tmu_pair_forward_ws": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int,
+                                   _vp, _vp, _f32, _vp, _vp, _vp, _f32, _vp, _vp, _int,
+                                   _vp, _vp, _sz, _int, _int, _int, _int, _vp]),
     "pair_transition": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "pair_transition_ws": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
     "pair_transition_workspace_bytes": (_sz, [_int, _int, _int, _int, _int]),
@@ -122,3 +130,38 @@ def stream_ptr(stream=None) -> int:
     import torch
     s = stream if stream is not None else torch.cuda.current_stream()
     return s.cuda_stream
+
+
+class KernelTimes:
+    """Kernel durations stamped by the runtime (``esm_timing_begin`` / ``esm_timing_end``):
+
+        with capi.KernelTimes(max_launches) as kt:
+            ...launches through this library...
+        kt.records  # [(kernel name, microseconds)] in launch order
+
+    Each timed launch carries start/stop events that the runtime stamps with the kernel's own
+    begin and end, so the figures are a profiler's kernel-trace durations, measured live."""
+
+    def __init__(self, max_launches: int):
+        self.max_launches = int(max_launches)
+        self.records: list[tuple[str, float]] = []
+
+    def __enter__(self):
+        check(lib().esm_timing_begin(self.max_launches))
+        return self
+
+    def __exit__(self, *exc):
+        h = lib()
+        us = (ctypes.c_float * max(self.max_launches, 1))()
+        n = ctypes.c_int(0)
+        rc = h.esm_timing_end(us, self.max_launches, ctypes.byref(n))
+        if exc[0] is None:
+            check(rc)
+        self.records = [(h.esm_timing_name(i).decode(), float(us[i])) for i in range(n.value)]
+        return False
+
+    def by_kernel(self) -> dict[str, list[float]]:
+        out: dict[str, list[float]] = {}
+        for name, t in self.records:
+            out.setdefault(name, []).append(t)
+        return out

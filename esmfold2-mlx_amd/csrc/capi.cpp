@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/esmfold2_amd.h"
 #include "kernels.h"
@@ -93,6 +94,31 @@ inline half_t* H(esm_half* p) { return reinterpret_cast<half_t*>(p); }
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 }  // namespace
+
+// Launch timing state (see ESM_LAUNCH in common.h): events created once and reused; a
+// session hands them out pairwise, in launch order, until esm_timing_end.
+namespace {
+struct TimingSession {
+  std::vector<hipEvent_t> events;
+  std::vector<std::string> names;
+  int used = 0, cap = 0;
+  bool armed = false;
+};
+thread_local TimingSession g_timing;
+}  // namespace
+
+namespace esm {
+bool timing_slot(const char* kernel_name, hipEvent_t* start, hipEvent_t* stop) {
+  TimingSession& t = g_timing;
+  if (!t.armed || t.used >= t.cap) return false;
+  *start = t.events[2 * t.used];
+  *stop = t.events[2 * t.used + 1];
+  std::string n(kernel_name);
+  if (n.size() >= 2 && n.front() == '(' && n.back() == ')') n = n.substr(1, n.size() - 2);
+  t.names[t.used++] = n;
+  return true;
+}
+}  // namespace esm
 
 extern "C" {
 
@@ -376,6 +402,42 @@ int tmu_pair_forward(const esm_half* z, const esm_half* mask, const float* o_ln_
   if (rc) return rc;
   return tmu_forward(out, mask, i_ln_in_w, i_ln_in_b, i_ln_in_eps, i_w_bundle, i_ln_mix_w, i_ln_mix_b, i_ln_mix_eps,
                      i_w_emit, i_w_gate, out, workspace, B, L, C, c, 0, 1, i_out_mask, stream);
+}
+
+// The sized forms: a workspace smaller than tmu_workspace_bytes(B, L, c) is refused before
+// anything else is looked at beyond the widths, so a buffer sized for another (B, L, c) or an
+// older layout is an error, not an overrun.
+static int tmu_ws_check(const char* fn, size_t have, int B, int L, int c) {
+  if (B <= 0 || L <= 0 || c <= 0 || c > 512) return 0;  // the unsized entry point reports these
+  const size_t need = tmu_workspace_bytes(B, L, c);
+  if (have < need)
+    return fail(ESM_ERR_SHAPE, "%s: workspace of %zu bytes, %zu needed for B=%d L=%d c=%d", fn, have, need, B, L, c);
+  return 0;
+}
+
+int tmu_forward_ws(const esm_half* z, const esm_half* mask, const float* ln_in_w, const float* ln_in_b,
+                   float ln_in_eps, const esm_half* w_bundle, const float* ln_mix_w, const float* ln_mix_b,
+                   float ln_mix_eps, const esm_half* w_emit, const esm_half* w_gate, esm_half* out, void* workspace,
+                   size_t workspace_bytes, int B, int L, int C, int c, int outgoing, int residual, int out_mask,
+                   void* stream) {
+  if (const int rc = tmu_ws_check("tmu_forward_ws", workspace_bytes, B, L, c)) return rc;
+  return tmu_forward(z, mask, ln_in_w, ln_in_b, ln_in_eps, w_bundle, ln_mix_w, ln_mix_b, ln_mix_eps, w_emit, w_gate,
+                     out, workspace, B, L, C, c, outgoing, residual, out_mask, stream);
+}
+
+int tmu_pair_forward_ws(const esm_half* z, const esm_half* mask, const float* o_ln_in_w, const float* o_ln_in_b,
+                        float o_ln_in_eps, const esm_half* o_w_bundle, const float* o_ln_mix_w,
+                        const float* o_ln_mix_b, float o_ln_mix_eps, const esm_half* o_w_emit,
+                        const esm_half* o_w_gate, int o_out_mask, const float* i_ln_in_w, const float* i_ln_in_b,
+                        float i_ln_in_eps, const esm_half* i_w_bundle, const float* i_ln_mix_w,
+                        const float* i_ln_mix_b, float i_ln_mix_eps, const esm_half* i_w_emit,
+                        const esm_half* i_w_gate, int i_out_mask, esm_half* out, void* workspace,
+                        size_t workspace_bytes, int B, int L, int C, int c, void* stream) {
+  if (const int rc = tmu_ws_check("tmu_pair_forward_ws", workspace_bytes, B, L, c)) return rc;
+  return tmu_pair_forward(z, mask, o_ln_in_w, o_ln_in_b, o_ln_in_eps, o_w_bundle, o_ln_mix_w, o_ln_mix_b,
+                          o_ln_mix_eps, o_w_emit, o_w_gate, o_out_mask, i_ln_in_w, i_ln_in_b, i_ln_in_eps, i_w_bundle,
+                          i_ln_mix_w, i_ln_mix_b, i_ln_mix_eps, i_w_emit, i_w_gate, i_out_mask, out, workspace, B, L,
+                          C, c, stream);
 }
 
 // Checks shared by the q8 GEMM entry points (fn names the caller in the messages); out is
@@ -711,6 +773,46 @@ int q8_dequant(const uint8_t* q, const esm_half* s, const esm_half* b, esm_half*
   if (!q || !s || !b || !w) return fail(ESM_ERR_NULL, "q8_dequant: NULL pointer");
   if (!aligned16(q) || !aligned16(w)) return fail(ESM_ERR_ALIGN, "q8_dequant: q, w must be 16-byte aligned");
   return hip_status(esm::launch_q8_dequant(q, H(s), H(b), H(w), N, K, (hipStream_t)stream), "q8_dequant launch");
+}
+
+int esm_timing_begin(int max_launches) {
+  if (max_launches < 0 || max_launches > (1 << 20))
+    return fail(ESM_ERR_SHAPE, "esm_timing_begin: max_launches=%d out of range", max_launches);
+  TimingSession& t = g_timing;
+  while ((int)t.events.size() < 2 * max_launches) {
+    hipEvent_t e;
+    const hipError_t err = hipEventCreate(&e);
+    if (err != hipSuccess) return hip_status(err, "esm_timing_begin: hipEventCreate");
+    t.events.push_back(e);
+  }
+  t.names.assign(max_launches, std::string());
+  t.used = 0;
+  t.cap = max_launches;
+  t.armed = true;
+  return ok();
+}
+
+int esm_timing_end(float* us, int cap, int* n) {
+  TimingSession& t = g_timing;
+  t.armed = false;
+  if (!n) return fail(ESM_ERR_NULL, "esm_timing_end: NULL n");
+  *n = 0;
+  const int m = t.used < cap ? t.used : cap;
+  if (m > 0 && !us) return fail(ESM_ERR_NULL, "esm_timing_end: NULL us");
+  for (int i = 0; i < m; ++i) {
+    hipError_t err = hipEventSynchronize(t.events[2 * i + 1]);
+    float ms = 0.f;
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, t.events[2 * i], t.events[2 * i + 1]);
+    if (err != hipSuccess) return hip_status(err, "esm_timing_end: event");
+    us[i] = ms * 1000.f;
+  }
+  *n = m;
+  return ok();
+}
+
+const char* esm_timing_name(int i) {
+  const TimingSession& t = g_timing;
+  return (i >= 0 && i < t.used) ? t.names[i].c_str() : "";
 }
 
 }  // extern "C"

@@ -12,8 +12,27 @@
 //   is a convention both operands follow.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+// --- launch timing (host side) ----------------------------------------------------------
+// While esm_timing_begin has armed the calling thread, each launch made through ESM_LAUNCH
+// takes the next pair of pre-created events and hands them to hipExtLaunchKernelGGL, which
+// stamps the kernel's own start and end into them: the elapsed times are the kernels'
+// durations as a profiler's kernel trace reports them, without the dispatch time an event
+// pair recorded around a launch adds. Unarmed, ESM_LAUNCH is hipLaunchKernelGGL.
+namespace esm {
+bool timing_slot(const char* kernel_name, hipEvent_t* start, hipEvent_t* stop);
+}
+#define ESM_LAUNCH(kernel, grid, block, lds, stream, ...)                                          \
+  do {                                                                                             \
+    hipEvent_t esm_t0_, esm_t1_;                                                                   \
+    if (esm::timing_slot(#kernel, &esm_t0_, &esm_t1_))                                             \
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, esm_t0_, esm_t1_, 0, __VA_ARGS__);   \
+    else                                                                                           \
+      hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                           \
+  } while (0)
 
 typedef _Float16 half_t;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));

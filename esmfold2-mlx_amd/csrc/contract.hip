@@ -258,11 +258,11 @@ __global__ __launch_bounds__(256, 2) void tmu_contract_frag_kernel(ContractArgs 
 hipError_t launch_contract(const ContractArgs& a, hipStream_t s) {
   if (a.frag) {
     const int nb = ((a.L + 31) / 32 + 3) / 4;
-    hipLaunchKernelGGL(tmu_contract_frag_kernel, dim3((unsigned)((long long)a.batch * nb * nb)), dim3(256), 0, s, a);
+    ESM_LAUNCH(tmu_contract_frag_kernel, dim3((unsigned)((long long)a.batch * nb * nb)), dim3(256), 0, s, a);
     return hipGetLastError();
   }
   const long long blocks = (long long)a.batch * ((a.L + BM - 1) / BM) * ((a.L + BN - 1) / BN);
-  hipLaunchKernelGGL(tmu_contract_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  ESM_LAUNCH(tmu_contract_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -302,13 +302,13 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_epilogue_kernel(EpilogueArgs p
 hipError_t launch_epilogue(const EpilogueArgs& a, int grid, hipStream_t s) {
   const bool m = a.out_mask && a.mask;
   if (m && a.residual)
-    hipLaunchKernelGGL((tmu_epilogue_kernel<true, true>), dim3(grid), dim3(NW * 64), 0, s, a);
+    ESM_LAUNCH((tmu_epilogue_kernel<true, true>), dim3(grid), dim3(NW * 64), 0, s, a);
   else if (m)
-    hipLaunchKernelGGL((tmu_epilogue_kernel<true, false>), dim3(grid), dim3(NW * 64), 0, s, a);
+    ESM_LAUNCH((tmu_epilogue_kernel<true, false>), dim3(grid), dim3(NW * 64), 0, s, a);
   else if (a.residual)
-    hipLaunchKernelGGL((tmu_epilogue_kernel<false, true>), dim3(grid), dim3(NW * 64), 0, s, a);
+    ESM_LAUNCH((tmu_epilogue_kernel<false, true>), dim3(grid), dim3(NW * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((tmu_epilogue_kernel<false, false>), dim3(grid), dim3(NW * 64), 0, s, a);
+    ESM_LAUNCH((tmu_epilogue_kernel<false, false>), dim3(grid), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 

@@ -411,27 +411,27 @@ __global__ __launch_bounds__(256) void esmc_swiglu_kernel(const half_t* __restri
 }
 
 hipError_t launch_esmc_ln(const EsmcLnArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(esmc_ln_kernel, dim3(a.M), dim3(NTR), 0, s, a);
+  ESM_LAUNCH(esmc_ln_kernel, dim3(a.M), dim3(NTR), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(esmc_qk_rope_kernel, dim3(a.B * a.L), dim3(NTR), 0, s, a);
+  ESM_LAUNCH(esmc_qk_rope_kernel, dim3(a.B * a.L), dim3(NTR), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_esmc_attention(const EsmcAttnArgs& a, hipStream_t s) {
   const dim3 grid(((a.L + 31) / 32) * a.B * a.H);
   if (a.L <= 256)  // one pass of 256 keys; longer sequences take passes of 512
-    hipLaunchKernelGGL(esmc_attention_kernel<8>, grid, dim3(256), 0, s, a);
+    ESM_LAUNCH(esmc_attention_kernel<8>, grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL(esmc_attention_kernel<16>, grid, dim3(256), 0, s, a);
+    ESM_LAUNCH(esmc_attention_kernel<16>, grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_esmc_swiglu(const half_t* x12, half_t* y, size_t M, int F, hipStream_t s) {
   const size_t n8 = M * (size_t)(F / 8), blocks = (n8 + 255) / 256;
-  hipLaunchKernelGGL(esmc_swiglu_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, x12, y, M, F);
+  ESM_LAUNCH(esmc_swiglu_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, x12, y, M, F);
   return hipGetLastError();
 }
 

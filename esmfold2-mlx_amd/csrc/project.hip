@@ -265,14 +265,14 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_project_kernel(ProjectArgs p) 
 hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s) {
   if (a.frag) {
     if (a.mask)
-      hipLaunchKernelGGL((tmu_project_kernel<true, true>), dim3(grid), dim3(NW * 64), 0, s, a);
+      ESM_LAUNCH((tmu_project_kernel<true, true>), dim3(grid), dim3(NW * 64), 0, s, a);
     else
-      hipLaunchKernelGGL((tmu_project_kernel<false, true>), dim3(grid), dim3(NW * 64), 0, s, a);
+      ESM_LAUNCH((tmu_project_kernel<false, true>), dim3(grid), dim3(NW * 64), 0, s, a);
   } else {
     if (a.mask)
-      hipLaunchKernelGGL((tmu_project_kernel<true, false>), dim3(grid), dim3(NW * 64), 0, s, a);
+      ESM_LAUNCH((tmu_project_kernel<true, false>), dim3(grid), dim3(NW * 64), 0, s, a);
     else
-      hipLaunchKernelGGL((tmu_project_kernel<false, false>), dim3(grid), dim3(NW * 64), 0, s, a);
+      ESM_LAUNCH((tmu_project_kernel<false, false>), dim3(grid), dim3(NW * 64), 0, s, a);
   }
   return hipGetLastError();
 }

@@ -326,7 +326,7 @@ hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N,
   const int ngroups = K / QG, ntiles = (N + kQ8TileN - 1) / kQ8TileN;
   const size_t total = (size_t)ntiles * ngroups * kQ8TileN;
   const size_t blocks = (total + 255) / 256;
-  hipLaunchKernelGGL(q8_pack_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st,
+  ESM_LAUNCH(q8_pack_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st,
                      reinterpret_cast<const uint16_t*>(s), reinterpret_cast<const uint16_t*>(b), sb, N, ngroups, total);
   return hipGetLastError();
 }
@@ -363,13 +363,13 @@ hipError_t q8_scratch_address(float** ptr) {
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s) {
   const int grid = a.mtiles * a.ntiles * a.splits;
   if (a.sb)
-    hipLaunchKernelGGL(q8_linear_kernel<true>, dim3(grid), dim3(NWQ * 64), 0, s, a);
+    ESM_LAUNCH(q8_linear_kernel<true>, dim3(grid), dim3(NWQ * 64), 0, s, a);
   else
-    hipLaunchKernelGGL(q8_linear_kernel<false>, dim3(grid), dim3(NWQ * 64), 0, s, a);
+    ESM_LAUNCH(q8_linear_kernel<false>, dim3(grid), dim3(NWQ * 64), 0, s, a);
   if (a.part && a.y) {  // partials and an fp16 output: sum them here (no y: the caller's consumer does)
     const size_t plane = (size_t)a.M * a.N, n4 = plane / 4;
     const size_t blocks = (n4 + 255) / 256;
-    hipLaunchKernelGGL(q8_reduce_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, s, a.part, a.y,
+    ESM_LAUNCH(q8_reduce_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, s, a.part, a.y,
                        n4, plane, a.splits);
   }
   return hipGetLastError();
@@ -423,7 +423,7 @@ hipError_t launch_q8_quantize(const float* w, uint8_t* q, half_t* s, half_t* b, 
   const size_t ngroups = (size_t)N * (K / QG);
   const size_t blocks = (ngroups * 16 + 255) / 256;
   const int grid = (int)(blocks < 8192 ? blocks : 8192);
-  hipLaunchKernelGGL(q8_quantize_kernel, dim3(grid), dim3(256), 0, st, w, q, s, b, ngroups);
+  ESM_LAUNCH(q8_quantize_kernel, dim3(grid), dim3(256), 0, st, w, q, s, b, ngroups);
   return hipGetLastError();
 }
 
@@ -432,7 +432,7 @@ hipError_t launch_q8_dequant(const uint8_t* q, const half_t* s, const half_t* b,
   const size_t nchunks = (size_t)N * K / 16;
   const size_t blocks = (nchunks + 255) / 256;
   const int grid = (int)(blocks < 4096 ? blocks : 4096);
-  hipLaunchKernelGGL(q8_dequant_kernel, dim3(grid), dim3(256), 0, st, q, s, b, w, nchunks, K);
+  ESM_LAUNCH(q8_dequant_kernel, dim3(grid), dim3(256), 0, st, q, s, b, w, nchunks, K);
   return hipGetLastError();
 }
 

@@ -367,9 +367,9 @@ __global__ __launch_bounds__(QT) void abs_diff_quantile_kernel(const float* __re
 
 hipError_t launch_parcae_step(const ParcaeArgs& a, int grid, hipStream_t s) {
   if (a.C == 128)
-    hipLaunchKernelGGL(parcae_step_kernel<128>, dim3(grid), dim3(256), 0, s, a);
+    ESM_LAUNCH(parcae_step_kernel<128>, dim3(grid), dim3(256), 0, s, a);
   else if (a.C == 256)
-    hipLaunchKernelGGL(parcae_step_kernel<256>, dim3(grid), dim3(256), 0, s, a);
+    ESM_LAUNCH(parcae_step_kernel<256>, dim3(grid), dim3(256), 0, s, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -377,20 +377,20 @@ hipError_t launch_parcae_step(const ParcaeArgs& a, int grid, hipStream_t s) {
 
 hipError_t launch_expected_distance(const DistoArgs& a, int grid, hipStream_t s) {
   if (a.nbins == 64 && a.C == 128)
-    hipLaunchKernelGGL((expected_distance_kernel<2, 128>), dim3(grid), dim3(256), 0, s, a);
+    ESM_LAUNCH((expected_distance_kernel<2, 128>), dim3(grid), dim3(256), 0, s, a);
   else if (a.nbins == 128 && a.C == 128)
-    hipLaunchKernelGGL((expected_distance_kernel<4, 128>), dim3(grid), dim3(256), 0, s, a);
+    ESM_LAUNCH((expected_distance_kernel<4, 128>), dim3(grid), dim3(256), 0, s, a);
   else if (a.nbins == 64 && a.C == 256)
-    hipLaunchKernelGGL((expected_distance_kernel<2, 256>), dim3(grid), dim3(256), 0, s, a);
+    ESM_LAUNCH((expected_distance_kernel<2, 256>), dim3(grid), dim3(256), 0, s, a);
   else if (a.nbins == 128 && a.C == 256)
-    hipLaunchKernelGGL((expected_distance_kernel<4, 256>), dim3(grid), dim3(256), 0, s, a);
+    ESM_LAUNCH((expected_distance_kernel<4, 256>), dim3(grid), dim3(256), 0, s, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 hipError_t launch_abs_diff_quantile(const float* x, const float* y, size_t n, float q, float* out, hipStream_t s) {
-  hipLaunchKernelGGL(abs_diff_quantile_kernel, dim3(1), dim3(QT), 0, s, x, y, n, q, out);
+  ESM_LAUNCH(abs_diff_quantile_kernel, dim3(1), dim3(QT), 0, s, x, y, n, q, out);
   return hipGetLastError();
 }
 

@@ -240,11 +240,11 @@ __global__ __launch_bounds__(NTT, 1) void transition_kernel(TransitionArgs p) {
 hipError_t launch_transition(const TransitionArgs& a, int grid, hipStream_t s) {
   const dim3 blk(NTT);
   if (a.w2 == nullptr && a.H == 512)
-    hipLaunchKernelGGL((transition_kernel<128, false>), dim3(grid), blk, 0, s, a);
+    ESM_LAUNCH((transition_kernel<128, false>), dim3(grid), blk, 0, s, a);
   else if (a.w2 == nullptr && a.H == 256)
-    hipLaunchKernelGGL((transition_kernel<64, false>), dim3(grid), blk, 0, s, a);
+    ESM_LAUNCH((transition_kernel<64, false>), dim3(grid), blk, 0, s, a);
   else if (a.w2 != nullptr && a.H == 256)
-    hipLaunchKernelGGL((transition_kernel<64, true>), dim3(grid), blk, 0, s, a);
+    ESM_LAUNCH((transition_kernel<64, true>), dim3(grid), blk, 0, s, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -755,9 +755,9 @@ hipError_t launch_ln_rows(const void* x, const float* x2, bool in_f32, const flo
 #define LN_ROWS_CASE(N)                                                                                    \
   case N:                                                                                                  \
     if (in_f32)                                                                                            \
-      hipLaunchKernelGGL((ln_rows_kernel<N, true>), dim3(grid), dim3(256), 0, s, x, x2, w, b, eps, out, rows); \
+      ESM_LAUNCH((ln_rows_kernel<N, true>), dim3(grid), dim3(256), 0, s, x, x2, w, b, eps, out, rows); \
     else                                                                                                   \
-      hipLaunchKernelGGL((ln_rows_kernel<N, false>), dim3(grid), dim3(256), 0, s, x, x2, w, b, eps, out, rows); \
+      ESM_LAUNCH((ln_rows_kernel<N, false>), dim3(grid), dim3(256), 0, s, x, x2, w, b, eps, out, rows); \
     break;
   switch (C / 128) {
     LN_ROWS_CASE(1)
@@ -777,16 +777,16 @@ hipError_t launch_ln_cf_to_cl(const half_t* x, int ldx, const float* w, const fl
   const int grid = (int)(tiles < 16384 ? tiles : 16384);
   switch (c) {
     case 128:
-      hipLaunchKernelGGL((ln_cf_to_cl_kernel<128>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
+      ESM_LAUNCH((ln_cf_to_cl_kernel<128>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
       break;
     case 256:
-      hipLaunchKernelGGL((ln_cf_to_cl_kernel<256>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
+      ESM_LAUNCH((ln_cf_to_cl_kernel<256>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
       break;
     case 384:
-      hipLaunchKernelGGL((ln_cf_to_cl_kernel<384>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
+      ESM_LAUNCH((ln_cf_to_cl_kernel<384>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
       break;
     case 512:
-      hipLaunchKernelGGL((ln_cf_to_cl_kernel<512>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
+      ESM_LAUNCH((ln_cf_to_cl_kernel<512>), dim3(grid), dim3(kCfThreads), 0, s, x, ldx, w, b, eps, y, B, L);
       break;
     default:
       return hipErrorInvalidValue;
@@ -817,25 +817,25 @@ static hipError_t launch_wide_gemm_ws(const WideArgs& a, int epi, int cus, hipSt
     case kWideGateCM:                                                                                        \
       if (!dual || sep) return hipErrorInvalidValue;                                                         \
       if (a.frag)                                                                                            \
-        hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideGateCM, true, false, KW, true>), grid, block, 0, s, a); \
+        ESM_LAUNCH((wide_gemm_ws_kernel<kWideGateCM, true, false, KW, true>), grid, block, 0, s, a); \
       else                                                                                                   \
-        hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideGateCM, true, false, KW>), grid, block, 0, s, a);       \
+        ESM_LAUNCH((wide_gemm_ws_kernel<kWideGateCM, true, false, KW>), grid, block, 0, s, a);       \
       break;                                                                                                 \
     case kWideResGate:                                                                                       \
       if (!dual || !sep) return hipErrorInvalidValue;                                                        \
-      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideResGate, true, true, KW>), grid, block, 0, s, a);         \
+      ESM_LAUNCH((wide_gemm_ws_kernel<kWideResGate, true, true, KW>), grid, block, 0, s, a);         \
       break;                                                                                                 \
     case kWideRelu:                                                                                          \
       if (dual) return hipErrorInvalidValue;                                                                 \
-      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideRelu, false, false, KW>), grid, block, 0, s, a);          \
+      ESM_LAUNCH((wide_gemm_ws_kernel<kWideRelu, false, false, KW>), grid, block, 0, s, a);          \
       break;                                                                                                 \
     case kWideSwiglu:                                                                                        \
       if (!dual || sep) return hipErrorInvalidValue;                                                         \
-      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideSwiglu, true, false, KW>), grid, block, 0, s, a);         \
+      ESM_LAUNCH((wide_gemm_ws_kernel<kWideSwiglu, true, false, KW>), grid, block, 0, s, a);         \
       break;                                                                                                 \
     case kWideResid:                                                                                         \
       if (dual) return hipErrorInvalidValue;                                                                 \
-      hipLaunchKernelGGL((wide_gemm_ws_kernel<kWideResid, false, false, KW>), grid, block, 0, s, a);         \
+      ESM_LAUNCH((wide_gemm_ws_kernel<kWideResid, false, false, KW>), grid, block, 0, s, a);         \
       break;                                                                                                 \
     default:                                                                                                 \
       return hipErrorInvalidValue;                                                                           \
@@ -857,23 +857,23 @@ hipError_t launch_wide_gemm(const WideArgs& a, int epi, hipStream_t s, int cus) 
   switch (epi) {
     case kWideGateCM:
       if (!dual || sep) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideGateCM, true, false, kWideBK>), grid, block, 0, s, a);
+      ESM_LAUNCH((wide_gemm_kernel<kWideGateCM, true, false, kWideBK>), grid, block, 0, s, a);
       break;
     case kWideResGate:
       if (!dual || !sep) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideResGate, true, true, kWideBK>), grid, block, 0, s, a);
+      ESM_LAUNCH((wide_gemm_kernel<kWideResGate, true, true, kWideBK>), grid, block, 0, s, a);
       break;
     case kWideRelu:
       if (dual) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideRelu, false, false, kWideBK>), grid, block, 0, s, a);
+      ESM_LAUNCH((wide_gemm_kernel<kWideRelu, false, false, kWideBK>), grid, block, 0, s, a);
       break;
     case kWideSwiglu:
       if (!dual || sep) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideSwiglu, true, false, kWideBK>), grid, block, 0, s, a);
+      ESM_LAUNCH((wide_gemm_kernel<kWideSwiglu, true, false, kWideBK>), grid, block, 0, s, a);
       break;
     case kWideResid:
       if (dual) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((wide_gemm_kernel<kWideResid, false, false, kWideBK>), grid, block, 0, s, a);
+      ESM_LAUNCH((wide_gemm_kernel<kWideResid, false, false, kWideBK>), grid, block, 0, s, a);
       break;
     default:
       return hipErrorInvalidValue;

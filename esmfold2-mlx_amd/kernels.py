@@ -139,6 +139,9 @@ def esmc_layer_norm(x, w, b, eps, y=None, alpha: float = 1.0, x_out=None, out=No
         _out(y, "y", F16, M * D)
     if y_parts is not None:
         _dev(y_parts[0], "y_parts", torch.float32)
+        gen = getattr(y_parts, "generation", None)
+        if gen is not None:  # partials living in the shared scratch: not overwritten since
+            scratch.check_generation(gen, y_parts[0].device, "esmc_layer_norm: y_parts")
         if y_parts[0].numel() < int(y_parts[1]) * M * D:
             raise capi.EsmError(-2, "esmc_layer_norm: y_parts smaller than splits x M x D")
     if y is not None or y_parts is not None:

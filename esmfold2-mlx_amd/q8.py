@@ -66,13 +66,26 @@ class Q8Linear(nn.Module):
         y = y.reshape(*lead, self.out_features)
         return y if x.dtype == torch.float16 else y.to(x.dtype)
 
-    def partials(self, x: torch.Tensor):
+    def partials(self, x: torch.Tensor) -> "ScratchParts":
         """(partials [splits, M, N] fp32, splits) of x . W^T for a consumer that sums them in split
         order (``kernels.esmc_layer_norm(..., y_parts=...)``): rounded to fp16, the sum is
-        ``forward(x)`` bit for bit. The view lives in the device's shared scratch: valid for work
-        queued after this call on the same stream until the next call of any module that uses
-        the scratch."""
+        ``forward(x)`` bit for bit. The view lives in the device's shared scratch: it must be
+        consumed before the next call of any module that uses the scratch on this device. The
+        result carries the scratch generation it was made in, and ``esmc_layer_norm`` refuses it
+        once the scratch has been handed out again."""
         x2 = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
         M = x2.shape[0]
         buf = scratch.get(kernels.q8_partials_bytes(M, self.in_features, self.out_features), x2.device)
-        return kernels.q8_linear_partials(x2, self.q, self.scales, self.biases, buf, GROUP, packed=self.packed)
+        gen = scratch.generation(x2.device)
+        parts, splits = kernels.q8_linear_partials(x2, self.q, self.scales, self.biases, buf, GROUP,
+                                                   packed=self.packed)
+        return ScratchParts(parts, splits, gen)
+
+
+class ScratchParts(tuple):
+    """``(partials, splits)`` in the shared scratch, tagged with the scratch generation."""
+
+    def __new__(cls, parts: torch.Tensor, splits: int, generation: int):
+        t = super().__new__(cls, (parts, splits))
+        t.generation = generation
+        return t

@@ -92,13 +92,13 @@ class TriMul(nn.Module):
         B, L, _, C = z16.shape
         if tuple(out.shape) != tuple(z16.shape) or out.dtype != F16 or not out.is_contiguous():
             raise capi.EsmError(-2, f"out must be a contiguous fp16 {tuple(z16.shape)} tensor")
-        base = self.workspace(B, L, z16.device).data_ptr()
-        capi.check(lib.tmu_forward(z16.data_ptr(), None if mask16 is None else mask16.data_ptr(),
-                                   self.ln_in_w.data_ptr(), self.ln_in_b.data_ptr(), self.ln_in_eps,
-                                   self.w_bundle.data_ptr(), self.ln_mix_w.data_ptr(), self.ln_mix_b.data_ptr(),
-                                   self.ln_mix_eps, self.w_emit.data_ptr(), self.w_gate.data_ptr(), out.data_ptr(),
-                                   base, B, L, C, self.c, int(self.outgoing), int(residual), int(self.out_mask),
-                                   capi.stream_ptr()))
+        ws = self.workspace(B, L, z16.device)
+        capi.check(lib.tmu_forward_ws(z16.data_ptr(), None if mask16 is None else mask16.data_ptr(),
+                                      self.ln_in_w.data_ptr(), self.ln_in_b.data_ptr(), self.ln_in_eps,
+                                      self.w_bundle.data_ptr(), self.ln_mix_w.data_ptr(), self.ln_mix_b.data_ptr(),
+                                      self.ln_mix_eps, self.w_emit.data_ptr(), self.w_gate.data_ptr(),
+                                      out.data_ptr(), ws.data_ptr(), ws.numel(), B, L, C, self.c,
+                                      int(self.outgoing), int(residual), int(self.out_mask), capi.stream_ptr()))
         return out
 
     def forward(self, pair_grid: torch.Tensor, visibility: torch.Tensor | None = None,
@@ -148,12 +148,12 @@ class TriMulPair(nn.Module):
 def run_pair(o: TriMul, i: TriMul, z16: torch.Tensor, mask16: torch.Tensor | None, out: torch.Tensor) -> torch.Tensor:
     """out = z1 + i(z1), z1 = z16 + o(z16) on the current stream (fp16; ``out`` may be ``z16``)."""
     B, L = z16.shape[0], z16.shape[1]
-    base = o.workspace(B, L, z16.device).data_ptr()
-    capi.check(capi.lib().tmu_pair_forward(
+    ws = o.workspace(B, L, z16.device)
+    capi.check(capi.lib().tmu_pair_forward_ws(
         z16.data_ptr(), None if mask16 is None else mask16.data_ptr(),
         o.ln_in_w.data_ptr(), o.ln_in_b.data_ptr(), o.ln_in_eps, o.w_bundle.data_ptr(), o.ln_mix_w.data_ptr(),
         o.ln_mix_b.data_ptr(), o.ln_mix_eps, o.w_emit.data_ptr(), o.w_gate.data_ptr(), int(o.out_mask),
         i.ln_in_w.data_ptr(), i.ln_in_b.data_ptr(), i.ln_in_eps, i.w_bundle.data_ptr(), i.ln_mix_w.data_ptr(),
         i.ln_mix_b.data_ptr(), i.ln_mix_eps, i.w_emit.data_ptr(), i.w_gate.data_ptr(), int(i.out_mask),
-        out.data_ptr(), base, B, L, o.C, o.c, capi.stream_ptr()))
+        out.data_ptr(), ws.data_ptr(), ws.numel(), B, L, o.C, o.c, capi.stream_ptr()))
     return out

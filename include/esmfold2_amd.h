@@ -201,6 +201,27 @@ int tmu_pair_forward(const esm_half* z, const esm_half* mask, const float* o_ln_
                      int c, void* stream);
 
 /*
+ * tmu_forward and tmu_pair_forward with the workspace's size: a workspace_bytes below
+ * tmu_workspace_bytes(B, L, c) returns ESM_ERR_SHAPE before any launch. The size depends on
+ * the width (the C >= 256 path keeps a fourth plane) and on the operand layout, so a caller
+ * that keeps its own buffer across shapes or library versions should use these forms.
+ * Same reference call sites as the unsized forms above.
+ */
+int tmu_forward_ws(const esm_half* z, const esm_half* mask, const float* ln_in_w, const float* ln_in_b,
+                   float ln_in_eps, const esm_half* w_bundle, const float* ln_mix_w, const float* ln_mix_b,
+                   float ln_mix_eps, const esm_half* w_emit, const esm_half* w_gate, esm_half* out, void* workspace,
+                   size_t workspace_bytes, int B, int L, int C, int c, int outgoing, int residual, int out_mask,
+                   void* stream);
+int tmu_pair_forward_ws(const esm_half* z, const esm_half* mask, const float* o_ln_in_w, const float* o_ln_in_b,
+                        float o_ln_in_eps, const esm_half* o_w_bundle, const float* o_ln_mix_w,
+                        const float* o_ln_mix_b, float o_ln_mix_eps, const esm_half* o_w_emit,
+                        const esm_half* o_w_gate, int o_out_mask, const float* i_ln_in_w, const float* i_ln_in_b,
+                        float i_ln_in_eps, const esm_half* i_w_bundle, const float* i_ln_mix_w,
+                        const float* i_ln_mix_b, float i_ln_mix_eps, const esm_half* i_w_emit,
+                        const esm_half* i_w_gate, int i_out_mask, esm_half* out, void* workspace,
+                        size_t workspace_bytes, int B, int L, int C, int c, void* stream);
+
+/*
  * Kernel (e): the pair transition, out = z + W3 act(W1 LN(z)) on every cell, with
  * act = ReLU (w2 == NULL: transformers' EsmFoldResidueMLP without biases, the
  * block-stack workload's 128 -> H -> 128 MLP) or SwiGLU, act = silu(W1 h) * (W2 h)
@@ -395,6 +416,20 @@ int q8_quantize(const float* w, uint8_t* q, esm_half* s, esm_half* b, int N, int
  */
 int q8_dequant(const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* w, int N, int K, int group,
                void* stream);
+
+/*
+ * Kernel timing for measurement (no counterpart in the reference, whose timings are wall
+ * clocks around whole folds, tools/bench_e2e.py:120-127). esm_timing_begin(n) arms the calling
+ * thread: its next n kernel launches through this library carry start/stop events that the
+ * runtime stamps with the kernel's own begin and end (hipExtLaunchKernelGGL), i.e. the
+ * durations a profiler's kernel trace reports. esm_timing_end waits for them and writes up to
+ * `cap` durations in microseconds, in launch order, and their count to *n; it disarms the
+ * thread. esm_timing_name(i) is the i-th timed launch's kernel name. Not for use under HIP
+ * graph capture. Events are created by the first begin and reused.
+ */
+int esm_timing_begin(int max_launches);
+int esm_timing_end(float* us, int cap, int* n);
+const char* esm_timing_name(int i);
 
 #ifdef __cplusplus
 }

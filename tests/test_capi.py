@@ -157,6 +157,26 @@ def test_pair_forward_validates_before_launching(lib):
     assert pair(B=1, L=4000) == -2                  # B * L * L * C >= 2^30
 
 
+def test_sized_forward_refuses_a_small_workspace(lib):
+    f, ws = ctypes.c_void_p(4096), ctypes.c_void_p(1 << 20)
+    o = [f, f, 1e-5, f, f, f, 1e-5, f, f, 0]
+
+    def fwd(nbytes, B=1, L=8, C=128, c=128):
+        return lib.tmu_forward_ws(f, None, f, f, 1e-5, f, f, f, 1e-5, f, f, f, ws, nbytes, B, L, C, c, 1, 1, 0, None)
+
+    def pair(nbytes, B=1, L=8, C=128, c=128):
+        return lib.tmu_pair_forward_ws(f, None, *o, *o, f, ws, nbytes, B, L, C, c, None)
+
+    for call in (fwd, pair):
+        need = lib.tmu_workspace_bytes(2, 40, 256)
+        assert call(need - 1, B=2, L=40, C=256, c=256) == -2 and "workspace" in _err(lib)
+        # a buffer sized for c = 128 is too small for the 256-wide path
+        assert call(lib.tmu_workspace_bytes(2, 40, 128), B=2, L=40, C=256, c=256) == -2
+        # empty and unsupported shapes keep the unsized forms' answers
+        assert call(0, B=0) == 0 and call(0, L=0) == 0
+        assert call(1 << 40, C=192, c=192) == -4
+
+
 def test_library_matches_its_sources(pkg):
     # the in-tree library carries the content hash of the sources it was compiled from
     lib = pkg.capi.lib(require_gpu=False)

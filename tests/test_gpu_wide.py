@@ -157,6 +157,43 @@ def test_transition_wide_matches_oracle(gpu_lib, pkg, C, H, swiglu):
     assert torch.equal(zz, out)
 
 
+@pytest.mark.parametrize("L", [129, 238])
+@pytest.mark.parametrize("swiglu", [True, False])
+def test_transition_256_h1024_across_line_tiles(gpu_lib, pkg, L, swiglu):
+    # the streaming wide GEMM (K = H = 1024 for the second GEMM) over several 128-cell line
+    # tiles, with a partial last tile: ESMFold2's real transition width at the pair sizes
+    C, H = 256, 1024
+    g = torch.Generator().manual_seed(L + 11 * swiglu)
+    z = torch.randn(1, L, L, C, generator=g).half()
+    w1 = torch.randn(H, C, generator=g) * C ** -0.5
+    w2 = torch.randn(H, C, generator=g) * C ** -0.5 if swiglu else None
+    w3 = torch.randn(C, H, generator=g) * H ** -0.5
+    lw, lb = 1 + 0.1 * torch.randn(C, generator=g), 0.1 * torch.randn(C, generator=g)
+    tr = pkg.trunk.PairTransition(lw, lb, w1, w3, w2=w2)
+    out = tr(z.to(DEV))
+    p = otr.TransitionWeights(lw.float(), lb.float(), w1.half().float(), w3.half().float(),
+                              None if w2 is None else w2.half().float())
+    with torch.no_grad():
+        ref = otr.transition(z.float(), p)
+    _bar(out, ref, z)
+
+
+@pytest.mark.parametrize("C,L", [(384, 129), (384, 257), (512, 65), (512, 129)])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_tmu_384_512_across_tiles(gpu_lib, pkg, C, L, outgoing):
+    # C = 384 and 512 run the streaming wide GEMM (K > 256) for the projection and emit/gate,
+    # and ln_cf_to_cl at its largest LDS footprint; random mask, random LN parameters, the
+    # oracle in fp32
+    p = _weights(C + L + outgoing, C, outgoing)
+    z = torch.randn(1, L, L, C, generator=torch.Generator().manual_seed(C + L)).half()
+    m = _mask(C + L + 2, 1, L, "random")
+    mod = pkg.trimul.TriMul.from_weights(p)
+    upd = mod(z.to(DEV), m.to(DEV))
+    with torch.no_grad():
+        ref = tmu.trimul(z.float(), m.float(), p, outgoing)
+    _bar(upd, ref, torch.zeros_like(ref))
+
+
 def test_transition_wide_needs_its_workspace(gpu_lib, pkg):
     lib = pkg.capi.lib()
     C, H, L = 256, 512, 8

@@ -54,12 +54,39 @@ def test_noalloc_allocates_nothing(gpu_lib, pkg):
     assert lib.q8_linear_noalloc(*args, pkg.capi.stream_ptr()) == 0
     torch.cuda.synchronize()
     before = torch.cuda.memory_allocated()
+    free_before = torch.cuda.mem_get_info()[0]  # the device's own count: sees a hipMalloc too
     for _ in range(3):
         assert lib.q8_linear_noalloc(*args, pkg.capi.stream_ptr()) == 0
     torch.cuda.synchronize()
     assert torch.cuda.memory_allocated() == before
+    assert torch.cuda.mem_get_info()[0] == free_before
     # argument checks come first, as for the other entry points
     assert lib.q8_linear_noalloc(None, None, None, None, None, None, 4, 128, 64, 64, None) == -1
     assert lib.q8_linear_noalloc(*args[:9], 32, pkg.capi.stream_ptr()) == -4
     bad = ctypes.c_void_p(y.data_ptr() + 2)
     assert lib.q8_linear_noalloc(*args[:5], bad, 238, 10240, 2560, 64, None) == -3
+
+
+def test_noalloc_captures_into_a_graph(gpu_lib, pkg):
+    """Captured with torch's default (global) capture mode, in which an allocation by the
+    library would fail the capture; every replay, with eager calls that share the static
+    scratch in between, equals the eager result bit for bit."""
+    lib = pkg.capi.lib()
+    x, q, s, b = _inputs(pkg, 238, 10240, 2560, seed=9)
+    x2, q2, s2, b2 = _inputs(pkg, 97, 10240, 2560, seed=10)
+    ref = _noalloc(pkg, lib, x, q, s, b, None)
+    ref2 = _noalloc(pkg, lib, x2, q2, s2, b2, None)
+    torch.cuda.synchronize()
+    y = torch.empty(238, 2560, dtype=torch.float16, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = lib.q8_linear_noalloc(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), None, y.data_ptr(),
+                                   238, 10240, 2560, 64, pkg.capi.stream_ptr())
+    assert rc == 0, lib.esm_last_error().decode()
+    for i in range(3):
+        y.zero_()
+        g.replay()
+        mid = _noalloc(pkg, lib, x2, q2, s2, b2, None)  # eager work on the same scratch between replays
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"replay {i}"
+        assert torch.equal(mid.view(torch.int16), ref2.view(torch.int16)), f"eager call after replay {i}"
