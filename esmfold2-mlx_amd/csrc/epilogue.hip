@@ -273,11 +273,15 @@ __global__ __launch_bounds__(NW * 64, 1) void tmu_epilogue_kernel(EpilogueArgs p
 
   // Consecutive units go to the waves of one workgroup: the two 32-cell halves of a
   // 128-byte line of x are then read on one CU (dealt to different XCDs, each half
-  // fetched the whole line again: 1.8x the compulsory reads).
+  // fetched the whole line again: 1.8x the compulsory reads). At 8 units per pair row a
+  // workgroup's units are one whole row of x per channel; rows are not line-aligned
+  // (ld = 240: 480 bytes), so the line at the end of row i is also the start of row i + 1,
+  // and the XCD-aware order puts consecutive rows on one XCD, whose L2 then fetches that
+  // line once.
   // Every wave passes the one barrier once: waves 0-3 with their first unit's loads in
   // flight, waves 4-7 after the staging.
   const int G = gridDim.x;
-  int u = blockIdx.x * NW + wave;
+  int u = xcd_remap(blockIdx.x, G) * NW + wave;
   if (wave < NW / 2) {
     UnitLoads ld;
     load_unit(u, ld);
