@@ -54,7 +54,11 @@ int cu_count() {
   return cached[dev];
 }
 
-constexpr int kMaxL = 4096;  // pair side limit: keeps every 32-bit tile index in range
+// Pair side limit. Every kernel addresses its tile, line or channel plane from a 64-bit base,
+// so nothing bounds B * L * L * C but memory; what L bounds is the 32-bit offset within one
+// such base: kernel (a) writes 32 channel planes of a fragment-layout tile from one base
+// (32 x 2 x L^2 bytes: 1.07 GB at 4096) and kernel (c) reads 16 channel rows (0.5 GB).
+constexpr int kMaxL = 4096;
 
 // q8 GEMM launch plan. A tile is kQ8TileM x kQ8TileN outputs; when the tiles alone
 // cannot fill the GPU, K is split over up to kQ8MaxSplits workgroups per tile (each
@@ -269,7 +273,6 @@ static int tmu_forward_wide(const esm_half* z, const esm_half* mask, const float
   hipStream_t st = (hipStream_t)stream;
   const int ld = tmu_leading_dim(L);
   const size_t ncell = (size_t)B * L * L;
-  if (ncell * C * 2 >= (1ull << 31)) return fail(ESM_ERR_SHAPE, "tmu_forward: B*L*L*C=%zu exceeds 2^30", ncell * C);
   const size_t plane = (size_t)B * c * tmu_plane_halfs(L);
   const size_t a256 = (plane * sizeof(esm_half) + 255) / 256 * 256 / sizeof(esm_half);
   half_t* wa = static_cast<half_t*>(workspace);
@@ -346,8 +349,10 @@ int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, c
     return fail(ESM_ERR_NULL, "tmu_forward: NULL pointer");
   if (!workspace) return fail(ESM_ERR_NULL, "tmu_forward: NULL workspace");
   if (L > kMaxL) return fail(ESM_ERR_SHAPE, "tmu_forward: L=%d exceeds %d", L, kMaxL);
-  if ((size_t)B * L * L * C >= (1ull << 30) || (long long)B * c > 65535)
-    return fail(ESM_ERR_SHAPE, "tmu_forward: B=%d L=%d C=%d: B*L*L*C must be < 2^30 and B*c <= 65535", B, L, C);
+  // No bound on B * L * L * C beyond memory: every kernel addresses its tile, line or channel
+  // plane from a 64-bit base, so each 32-bit buffer offset stays below 2 GB for L <= kMaxL.
+  if ((long long)B * c > 65535)
+    return fail(ESM_ERR_SHAPE, "tmu_forward: B=%d c=%d: B*c must be <= 65535", B, c);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
     return fail(ESM_ERR_ALIGN, "tmu_forward: workspace must be 256-byte aligned");
   if (!aligned16(z) || !aligned16(w_bundle) || !aligned16(w_emit) || !aligned16(w_gate) || !aligned16(out))
@@ -562,8 +567,7 @@ int pair_transition_ws(const esm_half* z, esm_half* out, const float* ln_w, cons
   if (B == 0 || L == 0) return ok();
   if (L > kMaxL) return fail(ESM_ERR_SHAPE, "pair_transition: L=%d exceeds %d", L, kMaxL);
   const size_t ncells = (size_t)B * L * L;
-  if (ncells * (C > hidden ? C : hidden) * 2 >= (1ull << 31))
-    return fail(ESM_ERR_SHAPE, "pair_transition: B*L*L=%zu cells exceed 2 GB of activations", ncells);
+  if (ncells / 32 > 0x7fffffffull) return fail(ESM_ERR_SHAPE, "pair_transition: B*L*L=%zu cells", ncells);
   if (!z || !out || !ln_w || !ln_b || !w1 || !w3) return fail(ESM_ERR_NULL, "pair_transition: NULL pointer");
   if (!aligned16(z) || !aligned16(out) || !aligned16(w1) || !aligned16(w3) || (w2 && !aligned16(w2)))
     return fail(ESM_ERR_ALIGN, "pair_transition: z, out, w1, w2, w3 must be 16-byte aligned");

@@ -127,14 +127,16 @@ __global__ __launch_bounds__(NTT, 1) void transition_kernel(TransitionArgs p) {
 
   // Thread -> (cell tid/16 + 16 i, channels ch0 .. ch0+7) for the loads, the LayerNorm,
   // the residual and the stores. Cells past the end load zeros and store nothing.
+  // The descriptors start at the tile's first cell, so the offsets stay small at any size
+  // (a tile past the end, the pipeline's last prefetch, uses tile 0's and loads nothing).
   const size_t ncells = p.ncells;
-  const rsrc_t rz = make_rsrc(p.z);
-  const rsrc_t ro = make_rsrc(p.out);
+  auto tile_base = [&](int tile) -> size_t { return (size_t)(tile < p.ntiles ? tile : 0) * TC * C; };
   auto cell_off = [&](int tile, int i) -> uint32_t {
-    const size_t cell = (size_t)tile * TC + (tid >> 4) + 16 * i;
-    return cell < ncells ? (uint32_t)(cell * C + ch0) * 2u : kOOB;
+    const int c = (tid >> 4) + 16 * i;
+    return (size_t)tile * TC + c < ncells ? (uint32_t)(c * C + ch0) * 2u : kOOB;
   };
   auto load_tile = [&](int tile, half8 (&zq)[2]) {
+    const rsrc_t rz = make_rsrc(p.z + tile_base(tile));
 #pragma unroll
     for (int i = 0; i < 2; i++) zq[i] = bload16(rz, cell_off(tile, i));
   };
@@ -222,7 +224,7 @@ __global__ __launch_bounds__(NTT, 1) void transition_kernel(TransitionArgs p) {
         o[e] = (half_t)(lo[e] + (float)zq[i][e]);
         o[e + 4] = (half_t)(hi[e] + (float)zq[i][e + 4]);
       }
-      bstore16(ro, cell_off(t, i), o);
+      bstore16(make_rsrc(p.out + tile_base(t)), cell_off(t, i), o);
     }
     __syncthreads();  // red and n_s are rewritten by the next tile
   };

@@ -139,13 +139,19 @@ __global__ __launch_bounds__(kCfThreads) void ln_cf_to_cl_kernel(const half_t* _
     const int bl = (int)(t / tpl);
     const int j0 = (int)(t - (long long)bl * tpl) * kCfCells;
     const int bi = bl / L, i = bl - bi * L;
-    // 1. c rows x 64 cells (8 pieces of 8 cells per row)
-    const rsrc_t rx = make_rsrc(x + ((size_t)bi * CC * L + i) * ldx + j0);
+    // 1. c rows x 64 cells (8 pieces of 8 cells per row). A wave's 64 lanes take 8 channel
+    //    rows per load; the descriptor starts at the first of them, so every offset stays
+    //    far below 2 GB whatever the size of the x planes.
+    const half_t* xt = x + ((size_t)bi * CC * L + i) * ldx + j0;
+    const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
 #pragma unroll
     for (int u = 0; u < NL; u++) {
       const int q = tid + kCfThreads * u, row = q / (kCfCells / 8), part = q % (kCfCells / 8);
+      const int row0 = (kCfThreads * u + 64 * wu) / (kCfCells / 8);  // the wave's first row
+      const rsrc_t rx = make_rsrc(xt + (size_t)row0 * L * ldx);
       const bool ok = j0 + 8 * part < ldx;
-      st16(&xs[row * XS + 8 * part], bload16(rx, ok ? (uint32_t)((size_t)row * L * ldx + 8 * part) * 2u : kOOB));
+      st16(&xs[row * XS + 8 * part],
+           bload16(rx, ok ? (uint32_t)((size_t)(row - row0) * L * ldx + 8 * part) * 2u : kOOB));
     }
     __syncthreads();
     // 2. this lane's channels of its cell (the lane names the piece of 4 cells at channel
@@ -266,7 +272,8 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
   const size_t cstride = p.transpose ? (size_t)L : 1;
   const int nvalid = L - pos0;               // cells of this tile inside the line
 
-  const rsrc_t rA1 = make_rsrc(p.a1), rA2 = make_rsrc(A2SEP ? p.a2 : p.a1);
+  // descriptors from the tile's first cell: offsets stay far below 2 GB at any grid size
+  const rsrc_t rA1 = make_rsrc(p.a1 + cell0 * K), rA2 = make_rsrc((A2SEP ? p.a2 : p.a1) + cell0 * K);
   const rsrc_t rW1 = make_rsrc(p.w1 + (size_t)n0 * K), rW2 = make_rsrc((DUAL ? p.w2 : p.w1) + (size_t)n0 * K);
   const int nk = (K + BK - 1) / BK;
 
@@ -279,7 +286,7 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_kernel(WideArgs p) {
     for (int u = 0; u < CH_A; u++) {
       const int id = tid + WNT * u, row = id / KC, k = kt * BK + (id % KC) * 8;
       const bool ok = live && row < nvalid && k < K;
-      const uint32_t off = ok ? (uint32_t)((cell0 + (size_t)row * cstride) * K + k) * 2u : kOOB;
+      const uint32_t off = ok ? (uint32_t)((size_t)row * cstride * K + k) * 2u : kOOB;
       r.a[0][u] = bload16(rA1, off);
       if constexpr (A2SEP) r.a[1][u] = bload16(rA2, off);
     }
@@ -520,8 +527,6 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   // single: W1 for outputs ob0 + 16 f .. +15. Lane: row l16 of the set, k = 32 ks + 8 q4 + e.
   half8 wf[2][KS];
 
-  const rsrc_t rA1 = make_rsrc(p.a1), rA2 = make_rsrc(A2SEP ? p.a2 : p.a1);
-  const rsrc_t rZ = make_rsrc(ZR ? (const void*)p.z : (const void*)p.a1);
   auto tile_coords = [&](int tile_v, int& bi, int& line, int& pos0) {
     const int tile = __builtin_amdgcn_readfirstlane(tile_v);  // uniform: keep the division scalar
     if constexpr (FRAG) {
@@ -556,29 +561,34 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
     half4 z[ZR ? NOB : 1][ZR ? 4 : 1];          // z[cell 16 cb + l16][outputs ob + 4 q4 .. +3]
   };
   // One tile's loads: the A rows (row-contiguous 16-byte pieces), and the residual pieces
-  // this lane adds, 8 bytes each.
+  // this lane adds, 8 bytes each. The descriptors start at the tile's first cell (line, pos0):
+  // every other cell of the tile lies after it (at most a few lines further), so the
+  // offsets stay far below 2 GB at any grid size.
   auto gload = [&](Regs& r, int tile) {
     const bool live = tile < ntiles;
     int bi, line, pos0;
     tile_coords(live ? tile : 0, bi, line, pos0);
+    const size_t c0 = cell_of(bi, line, pos0);
+    const rsrc_t rA1 = make_rsrc(p.a1 + c0 * K), rA2 = make_rsrc((A2SEP ? p.a2 : p.a1) + c0 * K);
 #pragma unroll
     for (int u = 0; u < CH_A; u++) {
       const int id = tid + WNT * u, row = id / (K / 8), j = id - row * (K / 8);
       int ln, ps;
       const bool ok = tcell(line, pos0, row, ln, ps) && live;
-      const uint32_t off = ok ? (uint32_t)(cell_of(bi, ln, ps) * K + 8 * j) * 2u : kOOB;
+      const uint32_t off = ok ? (uint32_t)((cell_of(bi, ln, ps) - c0) * K + 8 * j) * 2u : kOOB;
       r.a[0][u] = bload16(rA1, off);
       if constexpr (A2SEP) r.a[1][u] = bload16(rA2, off);
     }
     if constexpr (ZR) {
       const bool want = EPI == kWideResid || p.residual;
+      const rsrc_t rZ = make_rsrc(p.z + c0 * p.ldo);
 #pragma unroll
       for (int b = 0; b < NOB; b++)
 #pragma unroll
         for (int cb = 0; cb < 4; cb++) {
           const int c = 16 * cb + l16, o = n0 + ob0 + 16 * b + 4 * q4;
           const bool ok = want && live && pos0 + c < L && o < p.N;
-          const uint32_t off = ok ? (uint32_t)(cell_of(bi, line, pos0 + c) * p.ldo + o) * 2u : kOOB;
+          const uint32_t off = ok ? (uint32_t)((cell_of(bi, line, pos0 + c) - c0) * p.ldo + o) * 2u : kOOB;
           r.z[b][cb] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(rZ, (int)off, 0, 0));
         }
     }

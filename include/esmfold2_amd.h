@@ -170,7 +170,8 @@ int tmu_epilogue(const esm_half* x, int ldx, const esm_half* z, const esm_half* 
  * (ESMFold2's trunk is 256 wide, mlx_trunk.py:3-5): the wide path, five launches with
  * the same arithmetic (LN_in(z) -> gated projection stored channel-major -> kernel (b)
  * -> LN_mix over channels turned cell-major -> emit and gate GEMMs with the residual).
- * B * L * L * C < 2^30.
+ * L <= 4096 and B * c <= 65535; B * L * L * C is bounded only by memory (each kernel
+ * addresses its tile or channel plane from a 64-bit base).
  */
 int tmu_forward(const esm_half* z, const esm_half* mask, const float* ln_in_w, const float* ln_in_b, float ln_in_eps,
                 const esm_half* w_bundle, const float* ln_mix_w, const float* ln_mix_b, float ln_mix_eps,

@@ -156,6 +156,41 @@ def trimul(z: torch.Tensor, mask: torch.Tensor | None, p: TriMulWeights, outgoin
     return upd
 
 
+def trimul_cells(z: torch.Tensor, mask: torch.Tensor | None, p: TriMulWeights, cells, outgoing: bool | None = None,
+                 out_mask: bool = False) -> torch.Tensor:
+    """The update of ``trimul`` at the sampled cells ``cells`` = [(b, i, j), ...] only -> [n, C].
+
+    The same arithmetic (fast_trunk.py:19-32, mlx_trunk.py:84-90), restricted to what one output
+    cell reads: outgoing x[d,i,j] = sum_k a[d,i,k] b[d,j,k] needs the operands of rows i and j
+    of the pair grid, incoming x[d,i,j] = sum_k a[d,k,i] b[d,k,j] those of columns i and j; the
+    gate needs z[b,i,j]. Each distinct line is projected once, so a grid far too large for
+    ``trimul`` is checked at a few hundred cells in seconds. Pinned against ``trimul``
+    (tests/test_oracle_tmu.py)."""
+    if outgoing is None:
+        outgoing = p.outgoing
+    cells = [(int(b), int(i), int(j)) for b, i, j in cells]
+
+    def line(bi, r):  # the cells of row r (outgoing) or column r (incoming) of batch bi
+        return (z[bi, r], None if mask is None else mask[bi, r]) if outgoing else \
+            (z[bi, :, r], None if mask is None else mask[bi, :, r])
+
+    a_lines, b_lines = {}, {}
+    for bi, i, j in cells:
+        if (bi, i) not in a_lines:
+            zl, ml = line(bi, i)
+            a_lines[(bi, i)] = project(zl, ml, p)[1]   # a of the line: [L, c]
+        if (bi, j) not in b_lines:
+            zl, ml = line(bi, j)
+            b_lines[(bi, j)] = project(zl, ml, p)[2]   # b of the line: [L, c]
+    x = torch.stack([(a_lines[(bi, i)] * b_lines[(bi, j)]).sum(0) for bi, i, j in cells])  # [n, c]
+    zc = torch.stack([z[bi, i, j] for bi, i, j in cells])                                    # [n, C]
+    n = layer_norm(zc, p.ln_in_w, p.ln_in_b, p.ln_in_eps)
+    upd = F.linear(layer_norm(x, p.ln_mix_w, p.ln_mix_b, p.ln_mix_eps), p.w_emit) * torch.sigmoid(F.linear(n, p.w_gate))
+    if out_mask and mask is not None:
+        upd = upd * torch.stack([mask[bi, i, j] for bi, i, j in cells]).unsqueeze(-1)
+    return upd
+
+
 def trimul_pair(z, mask, p_out: TriMulWeights, p_in: TriMulWeights):
     """z1 = z + T_out(z); z2 = z1 + T_in(z1) (mlx_trunk.py:93-95)."""
     z1 = z + trimul(z, mask, p_out, True)

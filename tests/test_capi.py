@@ -154,7 +154,6 @@ def test_pair_forward_validates_before_launching(lib):
     assert pair(L=5000) == -2
     assert pair(z=ctypes.c_void_p(4096 + 2)) == -3
     assert pair(B=600) == -2                        # B * c beyond the contraction's grid
-    assert pair(B=1, L=4000) == -2                  # B * L * L * C >= 2^30
 
 
 def test_sized_forward_refuses_a_small_workspace(lib):

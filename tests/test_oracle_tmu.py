@@ -227,3 +227,25 @@ def test_crosscheck_catches_planted_mistakes(kind):
 
 def test_mutant_harness_is_sound():
     assert _hf_check(_mutant("none"), L=6, C=8, seed=100) == [False, False]
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("out_mask", [False, True])
+def test_sampled_cells_equal_the_full_update(outgoing, out_mask):
+    # trimul_cells (rows / columns i and j only) against trimul at every sampled cell, B = 2,
+    # random mask and LayerNorm parameters; the other direction's value differs
+    g = torch.Generator().manual_seed(21 + outgoing)
+    p = _rand_weights(g, 16, 16, outgoing)
+    B, L = 2, 9
+    z = torch.randn(B, L, L, 16, generator=g, dtype=D)
+    mask = _rand_mask(g, B, L)
+    full = tmu.trimul(z, mask, p, outgoing, out_mask=out_mask)
+    cells = [(b, i, j) for b in range(B) for i in (0, 3, L - 1) for j in (0, 4, L - 1)] + [(1, 5, 5)]
+    got = tmu.trimul_cells(z, mask, p, cells, outgoing, out_mask=out_mask)
+    ref = torch.stack([full[b, i, j] for b, i, j in cells])
+    torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
+    other = tmu.trimul_cells(z, mask, p, cells, not outgoing, out_mask=out_mask)
+    assert (other - ref).abs().max() > 1e-3
+    # no mask == all-ones mask
+    torch.testing.assert_close(tmu.trimul_cells(z, None, p, cells, outgoing),
+                               tmu.trimul_cells(z, torch.ones(B, L, L, dtype=D), p, cells, outgoing), rtol=0, atol=0)
