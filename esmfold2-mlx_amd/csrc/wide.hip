@@ -135,7 +135,11 @@ __global__ __launch_bounds__(kCfThreads) void ln_cf_to_cl_kernel(const half_t* _
     }
   const int tpl = (L + kCfCells - 1) / kCfCells;
   const long long ntiles = (long long)B * L * tpl;
-  for (long long t = blockIdx.x; t < ntiles; t += gridDim.x) {
+  // XCD-aware order: a tile's 128-byte pieces of x are not line-aligned (rows of ld halfs),
+  // so each line is shared with the neighbouring tile of the row or the next row; with
+  // consecutive tiles on one XCD its L2 fetches the line once (dealt round-robin, the
+  // reads were 1.8x the compulsory bytes)
+  for (long long t = xcd_remap(blockIdx.x, gridDim.x); t < ntiles; t += gridDim.x) {
     const int bl = (int)(t / tpl);
     const int j0 = (int)(t - (long long)bl * tpl) * kCfCells;
     const int bi = bl / L, i = bl - bi * L;

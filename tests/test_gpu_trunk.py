@@ -92,9 +92,20 @@ def test_block_stack_workload_full_size(gpu_lib, pkg):
     assert torch.isfinite(got.float()).all()
     with torch.no_grad():
         ref = otr.stack_forward(z.double(), None, _oracle_blocks(blocks), rc)
+        # the floor behind the 3e-2 bar, at this size: the reference's own fp16 scheme (every op
+        # output stored in fp16) and exact arithmetic with only the residual stream stored in
+        # fp16 both sit above 1e-2 x RMS(u) from fp64 in the max norm, near 2e-3 normwise
+        emu = otr.stack_forward_fp16ref(z.float(), None, _oracle_blocks(blocks, torch.float32), rc).double()
+        s16 = otr.stack_forward(z.double(), None, _oracle_blocks(blocks), rc, store=torch.float16)
+    rms = float((ref - z.double()).pow(2).mean().sqrt())
+    floors = []
+    for other in (emu, s16):
+        d = other - ref
+        floors.append(float(d.abs().max()) / rms)
+        assert 1e-2 < floors[-1] < 3e-2 and float(d.pow(2).mean().sqrt()) < 3e-3 * rms
     r = _check(got, z, ref, bar=3e-2, norm_bar=1e-2)
-    print(f"block stack L={L} {nb}x{rc}: max|err|/RMS(u) {r:.3e} against fp64 "
-          f"(the reference's fp16 scheme: 1.75e-2)")
+    print(f"block stack L={L} {nb}x{rc}: max|err|/RMS(u) {r:.3e} against fp64; the reference's fp16 "
+          f"scheme {floors[0]:.3e}, exact arithmetic with an fp16 stream {floors[1]:.3e}")
 
 
 def test_trunk_scratch_is_one_workspace(gpu_lib, pkg):
