@@ -419,6 +419,18 @@ def main():
             by = Nd * Kd + 2 * 2 * Nd * (Kd // 64) + 2 * L * Kd + 2 * L * Nd
             qres[name] = {"us": t * 1e6, "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
                           "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK, "split_k": ws is not None}
+            # each launch's own duration (runtime-stamped events, a pass of its own): with split-K the
+            # GEMM and the reduction of its partials separately, the reduction being the launch a
+            # consumer that sums the partials itself (the ESMC block's LayerNorm) does not make
+            nl = 20 * (2 if ws is not None else 1)
+            kq = pkg.capi.KernelTimes(nl)
+            torch.cuda.synchronize()
+            with kq:
+                for _ in range(20):
+                    K.q8_linear(xt, qt, st, bt, out=y, workspace=ws, packed=sbp)
+            torch.cuda.synchronize()
+            qres[name]["kernels_us"] = {k.split("<")[0].split("::")[-1]: statistics.fmean(v)
+                                        for k, v in kq.by_kernel().items()}
         # the quantiser (layer_params' mx.quantize) on the largest ESMC weight, w1 [10240, 2560] fp32:
         # reads 4 B per weight, writes a code per weight and an fp16 scale and bias per 64
         Nw, Kw = 10240, 2560

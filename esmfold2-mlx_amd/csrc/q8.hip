@@ -105,12 +105,14 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, kg = lane >> 5;
 
-  // Logical order: n-tile, then split, then m-tile fastest (XCD neighbours share codes).
+  // Logical order: split slowest, then n-tile, then m-tile fastest. XCD neighbours share
+  // codes (the m-tiles of one n-tile), and each K-split's workgroups fill whole XCDs, so
+  // a K-slice of x is fetched by the L2s of those XCDs only.
   int t = xcd_remap(blockIdx.x, gridDim.x);
   const int mt = t % p.mtiles;
   t /= p.mtiles;
-  const int sp = t % p.splits;
-  const int nt = t / p.splits;
+  const int nt = t % p.ntiles;
+  const int sp = t / p.ntiles;
   const int m0 = mt * kQ8TileM, n0 = nt * kQ8TileN;
   const int K = p.K, M = p.M, N = p.N, ngroups = K / QG;
   // This split's groups [sg0, sg1), walked two at a time.
