@@ -550,8 +550,15 @@ def main():
         t = e0.elapsed_time(e1) * 1e-3 / reps
         cw = alg_counts(L, 256, 256)
         fl = 2 * sum(v["flops"] for v in cw.values())
+        by = 2 * sum(v["bytes"] for v in cw.values())  # compulsory: the three fused kernels' bytes
+        tr = measured_traffic()  # counter bytes of the five launches per direction, when profiled
+        wide_keys = ("ln_rows_kernel", "wide_gemm_ws_kernel_gate_cm", "tmu_contract_frag_kernel_c256",
+                     "ln_cf_to_cl_kernel", "wide_gemm_ws_kernel_resgate")
+        meas = 2 * sum(tr[k] for k in wide_keys) if all(k in tr for k in wide_keys) else None
         out["pair_c256"] = {"us": t * 1e6, "cells_per_s": L * L / t, "tflops": fl / t / 1e12,
-                            "mfma_frac": fl / t / MFMA_F16_PEAK, "launches": 10,
+                            "mfma_frac": fl / t / MFMA_F16_PEAK,
+                            "compulsory_bytes": by, "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK,
+                            "traffic_bytes": meas, "launches": 10,
                             "workload": "TMU pair out+in with residuals, z [1,238,238,256] fp16, c_hidden 256"}
 
     esmc_case = None
