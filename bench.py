@@ -19,7 +19,10 @@ Also reported on the same JSON line:
                 contraction its fraction of its own roof, min(MFMA peak, AI x HBM
                 peak) with AI = L/3 FLOP/B by compulsory traffic;
   q8            the 8-bit ESMC-style linears [238,2560]x[2560->10240] and
-                [238,10240]x[10240->2560] (time, TFLOP/s, GB/s);
+                [238,10240]x[10240->2560] (time, TFLOP/s, GB/s) on the weight layout
+                Q8Linear keeps (codes and scales packed once per layer), the time
+                with the codes in MLX's [N, K] layout beside it, and each launch's
+                own duration;
   transition    the pair transition kernel (LN -> 128->512 -> ReLU -> 512->128 + z)
                 at L=238 (time, TFLOP/s, fraction of MFMA peak);
   block_stack   the pair-trunk block stack at L=238: 8 blocks of (T_out, T_in,
@@ -400,25 +403,33 @@ def main():
             xt, qt, st, bt = (t.to(dev) for t in (xq, qq, sq, bq))
             y = torch.empty(L, Nd, dtype=torch.float16, device=dev)
             ws = K.q8_workspace(L, Kd, Nd, device=dev)  # split-K partials when the tiles are too few
-            sbp = K.q8_pack_scales(st, bt)              # per-layer layout cache, built once
+            sbp = K.q8_pack_scales(st, bt)              # per-layer layout caches, built once, as Q8Linear
+            qpp = K.q8_pack_codes(qt)                   # does by default
             for _ in range(5):
-                K.q8_linear(xt, qt, st, bt, out=y, workspace=ws, packed=sbp)
+                K.q8_linear(xt, qt, st, bt, out=y, workspace=ws, packed=sbp, codes=qpp)
             rows = [0, L // 2, L - 1]
             name = f"{L}x{Kd}->{Nd}"
             q8_samples[name] = (rows, xq, qq, sq, bq, y[rows].double().cpu().numpy())
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
-            e0.record(stream)
             reps = 50
-            for _ in range(reps):
-                K.q8_linear(xt, qt, st, bt, out=y, workspace=ws, packed=sbp)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            t = e0.elapsed_time(e1) * 1e-3 / reps
+
+            def timed(codes):
+                torch.cuda.synchronize()
+                e0.record(stream)
+                for _ in range(reps):
+                    K.q8_linear(xt, qt, st, bt, out=y, workspace=ws, packed=sbp, codes=codes)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1) * 1e-3 / reps
+
+            t_nk = timed(None)  # the codes read in MLX's [N, K] layout (through LDS), the same bits
+            t = timed(qpp)
             fl = 2 * L * Kd * Nd
             by = Nd * Kd + 2 * 2 * Nd * (Kd // 64) + 2 * L * Kd + 2 * L * Nd
             qres[name] = {"us": t * 1e6, "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
-                          "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK, "split_k": ws is not None}
+                          "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK, "split_k": ws is not None,
+                          "layout": "packed codes and scales (Q8Linear's default)", "us_nk_codes": t_nk * 1e6}
             # each launch's own duration (runtime-stamped events, a pass of its own): with split-K the
             # GEMM and the reduction of its partials separately, the reduction being the launch a
             # consumer that sums the partials itself (the ESMC block's LayerNorm) does not make
@@ -427,7 +438,7 @@ def main():
             torch.cuda.synchronize()
             with kq:
                 for _ in range(20):
-                    K.q8_linear(xt, qt, st, bt, out=y, workspace=ws, packed=sbp)
+                    K.q8_linear(xt, qt, st, bt, out=y, workspace=ws, packed=sbp, codes=qpp)
             torch.cuda.synchronize()
             qres[name]["kernels_us"] = {k.split("<")[0].split("::")[-1]: statistics.fmean(v)
                                         for k, v in kq.by_kernel().items()}

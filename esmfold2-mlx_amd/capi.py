@@ -62,6 +62,10 @@ SIGNATURES = {
     "q8_linear_partials": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _int, _int, _int, _int, _vp]),
     "q8_packed_scales_bytes": (_sz, [_int, _int]),
     "q8_pack_scales": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp]),
+    "q8_packed_codes_bytes": (_sz, [_int, _int]),
+    "q8_pack_codes": (_int, [_vp, _vp, _int, _int, _int, _vp]),
+    "q8_linear_packed_ws": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
+    "q8_linear_packed_partials": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _int, _int, _int, _int, _vp]),
     "q8_dequant": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
     "q8_quantize": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
 }

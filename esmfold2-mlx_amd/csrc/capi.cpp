@@ -447,8 +447,17 @@ int tmu_pair_forward_ws(const esm_half* z, const esm_half* mask, const float* o_
 
 // Checks shared by the q8 GEMM entry points (fn names the caller in the messages); out is
 // y (8-byte aligned) or the partials (256-byte aligned). Sets *empty for a no-op shape.
+// With packed codes (qp) the weights are qp and sb, and q, s, b are not read.
+static int q8_check_weights(const char* fn, const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b,
+                            const uint32_t* sb, const uint8_t* qp, const void* out, unsigned out_align, int M, int K,
+                            int N, int group, bool* empty);
 static int q8_check(const char* fn, const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b,
                     const void* out, unsigned out_align, int M, int K, int N, int group, bool* empty) {
+  return q8_check_weights(fn, x, q, s, b, nullptr, nullptr, out, out_align, M, K, N, group, empty);
+}
+static int q8_check_weights(const char* fn, const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b,
+                            const uint32_t* sb, const uint8_t* qp, const void* out, unsigned out_align, int M, int K,
+                            int N, int group, bool* empty) {
   *empty = false;
   if (M < 0 || K < 0 || N < 0) return fail(ESM_ERR_SHAPE, "%s: M=%d K=%d N=%d must be >= 0", fn, M, K, N);
   if (group != 64) return fail(ESM_ERR_UNSUPPORTED, "%s: group=%d (supported: 64)", fn, group);
@@ -461,6 +470,13 @@ static int q8_check(const char* fn, const esm_half* x, const uint8_t* q, const e
   if (K > kQ8MaxK) return fail(ESM_ERR_SHAPE, "%s: K=%d too large (max %d)", fn, K, kQ8MaxK);
   if ((long long)N * K >= (1LL << 31) || (long long)M * K * 2 >= (1LL << 31))
     return fail(ESM_ERR_SHAPE, "%s: M=%d, K=%d, N=%d: x or q exceeds 2 GB", fn, M, K, N);
+  if (qp) {
+    if (!x || !sb || !out) return fail(ESM_ERR_NULL, "%s: NULL pointer", fn);
+    if (!aligned16(x) || !aligned16(qp) || !aligned16(sb) || (reinterpret_cast<uintptr_t>(out) & (out_align - 1)) != 0)
+      return fail(ESM_ERR_ALIGN, "%s: x, qp, sb must be 16-byte aligned and the output %u-byte aligned", fn,
+                  out_align);
+    return ok();
+  }
   if (!x || !q || !s || !b || !out) return fail(ESM_ERR_NULL, "%s: NULL pointer", fn);
   if (!aligned16(x) || !aligned16(q) || (reinterpret_cast<uintptr_t>(out) & (out_align - 1)) != 0 ||
       (reinterpret_cast<uintptr_t>(s) & 1u) != 0 || (reinterpret_cast<uintptr_t>(b) & 1u) != 0)
@@ -486,7 +502,7 @@ int q8_linear_ws(const esm_half* x, const uint8_t* q, const esm_half* s, const e
   }
   if (sb && !aligned16(sb)) return fail(ESM_ERR_ALIGN, "q8_linear: packed scales must be 16-byte aligned");
   esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits,
-                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb};
+                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb, nullptr};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear launch");
 }
 
@@ -508,7 +524,7 @@ int q8_linear_noalloc(const esm_half* x, const uint8_t* q, const esm_half* s, co
     const hipError_t e = esm::q8_scratch_address(&part);
     if (e != hipSuccess) return hip_status(e, "q8_linear_noalloc: scratch address");
   }
-  esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits, part, sb};
+  esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits, part, sb, nullptr};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_noalloc launch");
 }
 
@@ -531,8 +547,53 @@ int q8_linear_partials(const esm_half* x, const uint8_t* q, const esm_half* s, c
     return fail(ESM_ERR_SHAPE, "q8_linear_partials: %zu bytes for the partials, %zu needed", parts_bytes, pl.bytes);
   if (sb && !aligned16(sb)) return fail(ESM_ERR_ALIGN, "q8_linear_partials: packed scales must be 16-byte aligned");
   *splits = pl.splits;
-  esm::Q8Args a{H(x), q, H(s), H(b), nullptr, M, K, N, pl.mtiles, pl.ntiles, pl.splits, parts, sb};
+  esm::Q8Args a{H(x), q, H(s), H(b), nullptr, M, K, N, pl.mtiles, pl.ntiles, pl.splits, parts, sb, nullptr};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_partials launch");
+}
+
+int q8_linear_packed_ws(const esm_half* x, const uint8_t* qp, const uint32_t* sb, esm_half* y, int M, int K, int N,
+                        int group, void* workspace, size_t workspace_bytes, void* stream) {
+  bool empty;
+  if (!qp) return fail(ESM_ERR_NULL, "q8_linear_packed_ws: NULL packed codes");
+  if (const int rc = q8_check_weights("q8_linear_packed_ws", x, nullptr, nullptr, nullptr, sb, qp, y, 8, M, K, N, group,
+                                      &empty))
+    return rc;
+  if (empty) return ok();
+  Q8Plan pl = q8_plan(M, K, N);
+  if ((long long)pl.mtiles * pl.ntiles * pl.splits > 0x7fffffffLL)
+    return fail(ESM_ERR_SHAPE, "q8_linear_packed_ws: M=%d N=%d too large", M, N);
+  if (!workspace) {
+    pl.splits = 1;
+  } else if (pl.splits > 1) {
+    if (workspace_bytes < pl.bytes)
+      return fail(ESM_ERR_SHAPE, "q8_linear_packed_ws: workspace of %zu bytes, %zu needed", workspace_bytes, pl.bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(ESM_ERR_ALIGN, "q8_linear_packed_ws: workspace must be 256-byte aligned");
+  }
+  esm::Q8Args a{H(x), nullptr, nullptr, nullptr, H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits,
+                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb, qp};
+  return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_packed_ws launch");
+}
+
+int q8_linear_packed_partials(const esm_half* x, const uint8_t* qp, const uint32_t* sb, float* parts,
+                              size_t parts_bytes, int* splits, int M, int K, int N, int group, void* stream) {
+  bool empty;
+  if (!splits) return fail(ESM_ERR_NULL, "q8_linear_packed_partials: NULL splits");
+  *splits = 0;
+  if (!qp) return fail(ESM_ERR_NULL, "q8_linear_packed_partials: NULL packed codes");
+  if (const int rc = q8_check_weights("q8_linear_packed_partials", x, nullptr, nullptr, nullptr, sb, qp, parts, 256, M,
+                                      K, N, group, &empty))
+    return rc;
+  if (empty) return ok();
+  const Q8Plan pl = q8_plan(M, K, N);
+  if ((long long)pl.mtiles * pl.ntiles * pl.splits > 0x7fffffffLL)
+    return fail(ESM_ERR_SHAPE, "q8_linear_packed_partials: M=%d N=%d too large", M, N);
+  if (parts_bytes < pl.bytes)
+    return fail(ESM_ERR_SHAPE, "q8_linear_packed_partials: %zu bytes for the partials, %zu needed", parts_bytes,
+                pl.bytes);
+  *splits = pl.splits;
+  esm::Q8Args a{H(x), nullptr, nullptr, nullptr, nullptr, M, K, N, pl.mtiles, pl.ntiles, pl.splits, parts, sb, qp};
+  return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_packed_partials launch");
 }
 
 int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, esm_half* y, int M, int K,
@@ -748,6 +809,24 @@ int q8_pack_scales(const esm_half* s, const esm_half* b, uint32_t* sb, int N, in
   if ((reinterpret_cast<uintptr_t>(s) & 1u) || (reinterpret_cast<uintptr_t>(b) & 1u) || !aligned16(sb))
     return fail(ESM_ERR_ALIGN, "q8_pack_scales: s, b must be 2-byte and sb 16-byte aligned");
   return hip_status(esm::launch_q8_pack(H(s), H(b), sb, N, K, (hipStream_t)stream), "q8_pack_scales launch");
+}
+
+size_t q8_packed_codes_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 64 != 0 || K > kQ8MaxK || (long long)N * K >= (1LL << 31)) return 0;
+  return esm::q8_packed_codes_size(N, K);
+}
+
+int q8_pack_codes(const uint8_t* q, uint8_t* qp, int N, int K, int group, void* stream) {
+  if (N < 0 || K < 0) return fail(ESM_ERR_SHAPE, "q8_pack_codes: N=%d K=%d must be >= 0", N, K);
+  if (group != 64) return fail(ESM_ERR_UNSUPPORTED, "q8_pack_codes: group=%d (supported: 64)", group);
+  if (N == 0 || K == 0) return ok();
+  if (K % 64 != 0) return fail(ESM_ERR_SHAPE, "q8_pack_codes: K=%d must be a multiple of 64", K);
+  if (K > kQ8MaxK || (long long)N * K >= (1LL << 31))
+    return fail(ESM_ERR_SHAPE, "q8_pack_codes: N=%d K=%d: q exceeds 2 GB", N, K);
+  if (!q || !qp) return fail(ESM_ERR_NULL, "q8_pack_codes: NULL pointer");
+  if ((reinterpret_cast<uintptr_t>(q) & 7u) || !aligned16(qp))
+    return fail(ESM_ERR_ALIGN, "q8_pack_codes: q must be 8-byte and qp 16-byte aligned");
+  return hip_status(esm::launch_q8_pack_codes(q, qp, N, K, (hipStream_t)stream), "q8_pack_codes launch");
 }
 
 size_t q8_linear_workspace_bytes(int M, int K, int N) {

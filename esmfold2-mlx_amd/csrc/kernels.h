@@ -76,6 +76,7 @@ struct Q8Args {
   int splits;           // K ranges per tile
   float* part;          // [splits, M, N] fp32 partials, or nullptr: y written directly (splits 1)
   const uint32_t* sb;   // packed scales [ntiles, K/64, kQ8TileN] (b << 16 | s), or nullptr
+  const uint8_t* qp;    // codes packed by q8_pack_codes (needs sb), or nullptr: q is read
 };
 
 // q8 GEMM tile: kQ8TileM rows of x by kQ8TileN weight rows, kQ8Waves waves per workgroup.
@@ -208,6 +209,12 @@ hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s);
 hipError_t launch_esmc_attention(const EsmcAttnArgs& a, hipStream_t s);
 hipError_t launch_esmc_swiglu(const half_t* x12, half_t* y, size_t M, int F, hipStream_t s);
 hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st);
+// Bytes of q8_pack_codes' layout: per 160-row tile and step of two groups, 4 waves x 5
+// row blocks x 64 lanes x 16 bytes.
+constexpr size_t q8_packed_codes_size(int N, int K) {
+  return (size_t)((N + kQ8TileN - 1) / kQ8TileN) * (size_t)((K / 64 + 1) / 2) * (size_t)(kQ8Waves * 5 * 1024);
+}
+hipError_t launch_q8_pack_codes(const uint8_t* q, uint8_t* qp, int N, int K, hipStream_t st);
 hipError_t launch_ln_rows(const void* x, const float* x2, bool in_f32, const float* w, const float* b, float eps,
                           half_t* out, size_t rows, int C, hipStream_t s);
 hipError_t launch_ln_cf_to_cl(const half_t* x, int ldx, const float* w, const float* b, float eps, half_t* y, int B,

@@ -97,8 +97,15 @@ constexpr int SBT = 2 * kQ8TileN / 4;  // threads that load a step's packed scal
 // 16-byte load for 80 threads. Unpacked, every thread of the first 160 reads its row's
 // fp16 pairs from the [N, K/64] arrays: 160 scattered rows per step, several times the
 // L1 requests of the codes and x together.
-template <bool PACKED>
+//
+// PCODES: the codes come packed by q8_pack_codes, each MFMA A-fragment's 8 codes of both groups
+// of a step next to each other for its lane: a wave loads its 5 fragments of a step as 5 fully
+// coalesced 1 KB loads straight into registers (two steps ahead), and only x and the scales
+// pass through LDS (43 instead of 73 KB of LDS traffic per step). Same MFMAs in the same
+// order: the same bits as the [N, K] codes.
+template <bool PACKED, bool PCODES>
 __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
+  static_assert(PACKED || !PCODES, "packed codes are read with packed scales");
   __shared__ __align__(16) char smem[RED_BYTES];  // two step stages, then every wave's partial tile
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -115,16 +122,21 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
   const int sp = t / p.ntiles;
   const int m0 = mt * kQ8TileM, n0 = nt * kQ8TileN;
   const int K = p.K, M = p.M, N = p.N, ngroups = K / QG;
-  // This split's groups [sg0, sg1), walked two at a time.
-  const int sg0 = (int)((long long)ngroups * sp / p.splits);
-  const int sg1 = (int)((long long)ngroups * (sp + 1) / p.splits);
-  const int nsteps = (sg1 - sg0 + 1) / 2;
+  // This split's steps [st0, st1) of two groups each (whole steps, so a split starts where a
+  // packed step does), i.e. groups [sg0, sg1).
+  const int S = (ngroups + 1) / 2;
+  const int st0 = (int)((long long)S * sp / p.splits), st1 = (int)((long long)S * (sp + 1) / p.splits);
+  const int sg0 = 2 * st0, sg1 = 2 * st1 < ngroups ? 2 * st1 : ngroups;
+  const int nsteps = st1 - st0;
 
   // Buffer ranges end exactly at the arrays' ends: rows past M or N load zeros. The
   // second group of a step past sg1 (odd group count) loads zeros for x, so it adds 0.
-  const rsrc_t rq = make_rsrc_n(p.q + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
-  const rsrc_t rs = make_rsrc_n(p.s + (size_t)n0 * ngroups, (uint32_t)(N - n0) * (uint32_t)ngroups * 2u);
-  const rsrc_t rb = make_rsrc_n(p.b + (size_t)n0 * ngroups, (uint32_t)(N - n0) * (uint32_t)ngroups * 2u);
+  // (Arrays a mode does not read get a descriptor of range 0 on x: the caller may pass NULL.)
+  const rsrc_t rq = PCODES ? make_rsrc_n(p.x, 0u) : make_rsrc_n(p.q + (size_t)n0 * K, (uint32_t)(N - n0) * (uint32_t)K);
+  const rsrc_t rs = PACKED ? make_rsrc_n(p.x, 0u)
+                           : make_rsrc_n(p.s + (size_t)n0 * ngroups, (uint32_t)(N - n0) * (uint32_t)ngroups * 2u);
+  const rsrc_t rb = PACKED ? make_rsrc_n(p.x, 0u)
+                           : make_rsrc_n(p.b + (size_t)n0 * ngroups, (uint32_t)(N - n0) * (uint32_t)ngroups * 2u);
   const rsrc_t rx = make_rsrc_n(p.x + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K * 2u);
   const rsrc_t rsb = make_rsrc_n(PACKED ? (const void*)(p.sb + (size_t)nt * ngroups * kQ8TileN) : (const void*)p.x,
                                  PACKED ? (uint32_t)ngroups * kQ8TileN * 4u : 0u);
@@ -212,28 +224,107 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     }
   };
 
-  // Pipeline: step s+2's loads in flight while step s computes from LDS and step s+1's
-  // registers wait to be stored; one barrier per step. Unrolled by two (register sets
-  // A and B), a single loop exit, the leftover step after it.
-  Q8Load la, lb;
-  if (nsteps > 0) {
-    gload(la, 0);
-    gload(lb, 1);
-    sstore(la, 0);
-    __syncthreads();
+  if constexpr (!PCODES) {
+    // Pipeline: step s+2's loads in flight while step s computes from LDS and step s+1's
+    // registers wait to be stored; one barrier per step. Unrolled by two (register sets
+    // A and B), a single loop exit, the leftover step after it.
+    Q8Load la, lb;
+    if (nsteps > 0) {
+      gload(la, 0);
+      gload(lb, 1);
+      sstore(la, 0);
+      __syncthreads();
+    }
+    int st = 0;
+    for (; st + 2 <= nsteps; st += 2) {
+      gload(la, st + 2);
+      compute(0);
+      sstore(lb, 1);
+      __syncthreads();
+      gload(lb, st + 3);
+      compute(1);
+      sstore(la, 0);
+      __syncthreads();
+    }
+    if (st < nsteps) compute(0);
+  } else {
+    // Codes of step s (this wave's 5 fragments) in register set A or B from two steps before;
+    // x and the scales staged as above, in a stage without the codes area.
+    constexpr int XS = XSTAGE + SBSTAGE;
+    constexpr size_t kStepBytes = (size_t)NWQ * NBQ * 1024;  // one step of one n-tile
+    const rsrc_t rqp = make_rsrc_n(p.qp + ((size_t)nt * S + st0) * kStepBytes, (uint32_t)(nsteps * kStepBytes));
+    auto gcodes = [&](u32x4 (&cq)[NBQ], int step) {
+#pragma unroll
+      for (int nb = 0; nb < NBQ; nb++)
+        cq[nb] = __builtin_amdgcn_raw_buffer_load_b128(
+            rqp, (int)(step < nsteps ? (uint32_t)(((step * NWQ + wave) * NBQ + nb) * 1024 + lane * 16) : kOOB), 0, 0);
+    };
+    auto xload = [&](u32x4 (&xv)[XCH], u32x4& sbv, int step) {
+      const int g = sg0 + 2 * step;
+      const bool two = g + 1 < sg1;
+#pragma unroll
+      for (int i = 0; i < XCH; i++) {
+        const int c = tid + NT * i, row = c >> 4, j = c & 15;
+        const uint32_t off = (j < 8 || two) ? ((uint32_t)row * K + g * QG) * 2u + 16u * j : kOOB;
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+      }
+      sbv = __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(tid < SBT ? ((uint32_t)g * kQ8TileN + 4u * tid) * 4u : kOOB),
+                                                  0, 0);
+    };
+    auto xstore = [&](const u32x4 (&xv)[XCH], const u32x4& sbv, int buf) {
+      char* st = smem + buf * XS;
+#pragma unroll
+      for (int i = 0; i < XCH; i++) {
+        const int c = tid + NT * i, row = c >> 4, j = c & 15;
+        *reinterpret_cast<u32x4*>(st + row * XSTR + 16 * j) = xv[i];
+      }
+      if (tid < SBT) *reinterpret_cast<u32x4*>(reinterpret_cast<uint32_t*>(st + XSTAGE) + 4 * tid) = sbv;
+    };
+    auto compute_pc = [&](int buf, const u32x4 (&cq)[NBQ]) {
+      const char* st = smem + buf * XS;
+      const uint32_t* sb = reinterpret_cast<const uint32_t*>(st + XSTAGE);
+#pragma unroll
+      for (int g = 0; g < 2; g++) {
+        half8 a[NBQ];
+#pragma unroll
+        for (int nb = 0; nb < NBQ; nb++) {
+          const uint32_t w = sb[g * kQ8TileN + 32 * nb + r];
+          a[nb] = dequant8(cq[nb][2 * g], cq[nb][2 * g + 1], splat2(w & 0xffffu), splat2(w >> 16));
+        }
+        half8 xf[MBQ];
+#pragma unroll
+        for (int mb = 0; mb < MBQ; mb++)
+          xf[mb] = *reinterpret_cast<const half8*>(st + (32 * mb + r) * XSTR + 128 * g + 32 * wave + 16 * kg);
+#pragma unroll
+        for (int nb = 0; nb < NBQ; nb++)
+#pragma unroll
+          for (int mb = 0; mb < MBQ; mb++) acc[mb][nb] = mfma32(a[nb], xf[mb], acc[mb][nb]);
+      }
+    };
+    u32x4 xa[XCH], xb[XCH], sa, sbb, ca[NBQ], cb[NBQ];
+    if (nsteps > 0) {
+      xload(xa, sa, 0);
+      gcodes(ca, 0);
+      xload(xb, sbb, 1);
+      gcodes(cb, 1);
+      xstore(xa, sa, 0);
+      __syncthreads();
+    }
+    int st = 0;
+    for (; st + 2 <= nsteps; st += 2) {
+      xload(xa, sa, st + 2);
+      compute_pc(0, ca);
+      gcodes(ca, st + 2);
+      xstore(xb, sbb, 1);
+      __syncthreads();
+      xload(xb, sbb, st + 3);
+      compute_pc(1, cb);
+      gcodes(cb, st + 3);
+      xstore(xa, sa, 0);
+      __syncthreads();
+    }
+    if (st < nsteps) compute_pc(0, ca);
   }
-  int st = 0;
-  for (; st + 2 <= nsteps; st += 2) {
-    gload(la, st + 2);
-    compute(0);
-    sstore(lb, 1);
-    __syncthreads();
-    gload(lb, st + 3);
-    compute(1);
-    sstore(la, 0);
-    __syncthreads();
-  }
-  if (st < nsteps) compute(0);
   __syncthreads();  // the stages are reused as the reduction area
 
   // The 4 partial tiles -> LDS; wave w then finishes blocks w, w+4, w+8.
@@ -324,6 +415,41 @@ __global__ __launch_bounds__(256) void q8_pack_kernel(const uint16_t* __restrict
   }
 }
 
+// Codes in the order q8_linear_kernel<true, true> reads them: chunk ((t S + s) 4 + w) 5 + nb,
+// lane l, 16 bytes = the codes of row 160 t + 32 nb + l % 32 at k = 128 s + 16 w + 8 (l / 32)
+// + 0..7 (group 2s), then the same k + 64 (group 2s+1); zeros past N and past K. One thread
+// per 16-byte chunk.
+__global__ __launch_bounds__(256) void q8_pack_codes_kernel(const uint8_t* __restrict__ q, uint8_t* __restrict__ qp,
+                                                            int N, int K, size_t nchunks) {
+  const int S = (K / QG + 1) / 2;
+  for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < nchunks; c += (size_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(c % 64);
+    size_t rest = c / 64;
+    const int nb = (int)(rest % NBQ);
+    rest /= NBQ;
+    const int w = (int)(rest % NWQ);
+    rest /= NWQ;
+    const int s = (int)(rest % S);
+    const int t = (int)(rest / S);
+    const int n = t * kQ8TileN + 32 * nb + (lane & 31);
+    const int k0 = 128 * s + 16 * w + 8 * (lane >> 5);
+    u32x2 lo = {0u, 0u}, hi = {0u, 0u};
+    if (n < N) {
+      lo = *reinterpret_cast<const u32x2*>(q + (size_t)n * K + k0);
+      if (k0 + 64 < K) hi = *reinterpret_cast<const u32x2*>(q + (size_t)n * K + k0 + 64);
+    }
+    *reinterpret_cast<u32x4*>(qp + c * 16) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+  }
+}
+
+hipError_t launch_q8_pack_codes(const uint8_t* q, uint8_t* qp, int N, int K, hipStream_t st) {
+  const size_t nchunks = q8_packed_codes_size(N, K) / 16;
+  const size_t blocks = (nchunks + 255) / 256;
+  ESM_LAUNCH(q8_pack_codes_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st, q, qp, N, K,
+             nchunks);
+  return hipGetLastError();
+}
+
 hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st) {
   const int ngroups = K / QG, ntiles = (N + kQ8TileN - 1) / kQ8TileN;
   const size_t total = (size_t)ntiles * ngroups * kQ8TileN;
@@ -364,10 +490,13 @@ hipError_t q8_scratch_address(float** ptr) {
 
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s) {
   const int grid = a.mtiles * a.ntiles * a.splits;
-  if (a.sb)
-    ESM_LAUNCH(q8_linear_kernel<true>, dim3(grid), dim3(NWQ * 64), 0, s, a);
+  if (a.qp && !a.sb) return hipErrorInvalidValue;
+  if (a.qp)
+    ESM_LAUNCH((q8_linear_kernel<true, true>), dim3(grid), dim3(NWQ * 64), 0, s, a);
+  else if (a.sb)
+    ESM_LAUNCH((q8_linear_kernel<true, false>), dim3(grid), dim3(NWQ * 64), 0, s, a);
   else
-    ESM_LAUNCH(q8_linear_kernel<false>, dim3(grid), dim3(NWQ * 64), 0, s, a);
+    ESM_LAUNCH((q8_linear_kernel<false, false>), dim3(grid), dim3(NWQ * 64), 0, s, a);
   if (a.part && a.y) {  // partials and an fp16 output: sum them here (no y: the caller's consumer does)
     const size_t plane = (size_t)a.M * a.N, n4 = plane / 4;
     const size_t blocks = (n4 + 255) / 256;

@@ -270,10 +270,22 @@ def q8_partials_buffer(M: int, K: int, N: int, device=None):
                        device=device if device is not None else "cuda")
 
 
-def q8_linear_partials(x, q, s, b, parts, group: int = 64, packed=None):
+def _packed_codes(lib, fn, codes, packed, N, K):
+    """Device pointer of packed codes (``q8_pack_codes``), which are read with packed scales."""
+    _dev(codes, "codes", torch.uint8)
+    if packed is None:
+        raise capi.EsmError(-2, f"{fn}: packed codes need the packed scales too")
+    if codes.numel() < lib.q8_packed_codes_bytes(N, K):
+        raise capi.EsmError(-2, f"{fn}: packed codes too small for this shape")
+    return codes.data_ptr()
+
+
+def q8_linear_partials(x, q, s, b, parts, group: int = 64, packed=None, codes=None):
     """Kernel (d) without its split reduction: returns (partials [splits, M, N] fp32, splits), a view
     of ``parts`` (a uint8 buffer of at least q8_linear_partials_bytes + 256 bytes, e.g. from
-    ``q8_partials_buffer`` or ``q8_workspace``). fp16(sum over splits in order) is q8_linear's y."""
+    ``q8_partials_buffer`` or ``q8_workspace``). fp16(sum over splits in order) is q8_linear's y.
+    ``codes`` (from ``q8_pack_codes``, with ``packed``) reads the weights in the packed order: the
+    same bits."""
     lib = capi.lib()
     _dev(x, "x", F16)
     _dev(q, "q", torch.uint8)
@@ -292,9 +304,14 @@ def q8_linear_partials(x, q, s, b, parts, group: int = 64, packed=None):
             raise capi.EsmError(-2, "q8_linear_partials: packed scales too small for this shape")
         sbp = packed.data_ptr()
     splits = ctypes.c_int(0)
-    capi.check(lib.q8_linear_partials(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), sbp,
-                                      parts.data_ptr() + off, parts.numel() - off, ctypes.byref(splits), M, K, N,
-                                      group, capi.stream_ptr()))
+    if codes is not None:
+        qp = _packed_codes(lib, "q8_linear_partials", codes, packed, N, K)
+        capi.check(lib.q8_linear_packed_partials(x.data_ptr(), qp, sbp, parts.data_ptr() + off, parts.numel() - off,
+                                                 ctypes.byref(splits), M, K, N, group, capi.stream_ptr()))
+    else:
+        capi.check(lib.q8_linear_partials(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), sbp,
+                                          parts.data_ptr() + off, parts.numel() - off, ctypes.byref(splits), M, K, N,
+                                          group, capi.stream_ptr()))
     n = splits.value
     return parts[off:off + 4 * n * M * N].view(torch.float32).view(n, M, N), n
 
@@ -313,10 +330,25 @@ def q8_pack_scales(s, b, group: int = 64):
     return sb
 
 
-def q8_linear(x, q, s, b, group: int = 64, out=None, workspace=None, packed=None):
+def q8_pack_codes(q, group: int = 64):
+    """Codes [N, K] uint8 in the order kernel (d)'s matrix-core fragments take them (a layout
+    cache, about N*K bytes; read together with ``q8_pack_scales``' words)."""
+    lib = capi.lib()
+    _dev(q, "q", torch.uint8)
+    N, K = q.shape
+    n = int(lib.q8_packed_codes_bytes(N, K))
+    if n == 0:
+        raise capi.EsmError(-2, f"q8_pack_codes: unsupported shape q{tuple(q.shape)}")
+    qp = torch.empty(n, dtype=torch.uint8, device=q.device)
+    capi.check(lib.q8_pack_codes(q.data_ptr(), qp.data_ptr(), N, K, group, capi.stream_ptr()))
+    return qp
+
+
+def q8_linear(x, q, s, b, group: int = 64, out=None, workspace=None, packed=None, codes=None):
     """Kernel (d): y = x . W^T, W = s*q + b per group of 64 along K (fp16 in/out, fp32 accumulation).
-    ``packed`` (from ``q8_pack_scales``) and ``workspace`` (from ``q8_workspace``) are optional
-    speed-ups; the result is the same bits with or without them."""
+    ``packed`` (from ``q8_pack_scales``), ``codes`` (from ``q8_pack_codes``, used with ``packed``) and
+    ``workspace`` (from ``q8_workspace``) are optional speed-ups; the result is the same bits with
+    or without them."""
     lib = capi.lib()
     _dev(x, "x", F16)
     _dev(q, "q", torch.uint8)
@@ -339,8 +371,13 @@ def q8_linear(x, q, s, b, group: int = 64, out=None, workspace=None, packed=None
         if packed.numel() * 4 < lib.q8_packed_scales_bytes(N, K):
             raise capi.EsmError(-2, "q8_linear: packed scales too small for this shape")
         sbp = packed.data_ptr()
-    capi.check(lib.q8_linear_ws(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), sbp, y.data_ptr(), M, K, N,
-                                group, wp, wn, capi.stream_ptr()))
+    if codes is not None:
+        qp = _packed_codes(lib, "q8_linear", codes, packed, N, K)
+        capi.check(lib.q8_linear_packed_ws(x.data_ptr(), qp, sbp, y.data_ptr(), M, K, N, group, wp, wn,
+                                           capi.stream_ptr()))
+    else:
+        capi.check(lib.q8_linear_ws(x.data_ptr(), q.data_ptr(), s.data_ptr(), b.data_ptr(), sbp, y.data_ptr(), M, K,
+                                    N, group, wp, wn, capi.stream_ptr()))
     return y
 
 

@@ -7,9 +7,12 @@ input axis of torch's [out, in] layout with fp16 scales and biases
 [N, K], which is the little-endian byte view of MLX's uint32 packing) and
 computes y = x . W^T with W = s*q + b on the gfx950 kernel: fp16 activations,
 fp32 accumulation, fp16 output. The scales and biases are packed once per layer
-into the kernel's per-tile layout, and shapes whose output tiles cannot fill the
-GPU split K over more workgroups through the device's shared scratch (one buffer
-for every layer, sized for the largest call).
+into the kernel's per-tile layout, and by default the codes too, into the order of
+the kernel's matrix-core fragments (a second copy of the codes, N*K bytes: the
+kernel then loads them straight into registers; ``pack_codes=False`` keeps one
+copy and reads the [N, K] codes through LDS, the same bits). Shapes whose output
+tiles cannot fill the GPU split K over more workgroups through the device's
+shared scratch (one buffer for every layer, sized for the largest call).
 """
 
 from __future__ import annotations
@@ -23,7 +26,8 @@ GROUP = 64
 
 
 class Q8Linear(nn.Module):
-    def __init__(self, q: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, device=None):
+    def __init__(self, q: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, device=None,
+                 pack_codes: bool = True):
         super().__init__()
         N, K = q.shape
         if K % GROUP or N % 64 or tuple(scales.shape) != (N, K // GROUP) or tuple(biases.shape) != (N, K // GROUP):
@@ -34,6 +38,7 @@ class Q8Linear(nn.Module):
         self.register_buffer("biases", biases.detach().to(device=dev, dtype=torch.float16).contiguous())
         self.in_features, self.out_features = K, N
         self.register_buffer("packed", kernels.q8_pack_scales(self.scales, self.biases, GROUP))
+        self.register_buffer("codes_packed", kernels.q8_pack_codes(self.q, GROUP) if pack_codes else None)
 
     @classmethod
     def from_float(cls, w: torch.Tensor, **kw) -> "Q8Linear":
@@ -62,7 +67,8 @@ class Q8Linear(nn.Module):
         M = x2.shape[0]
         n = kernels.q8_workspace_bytes(M, self.in_features, self.out_features)
         ws = scratch.get(n, x2.device) if n else None  # split-K partials, only while this call runs
-        y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP, workspace=ws, packed=self.packed)
+        y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP, workspace=ws, packed=self.packed,
+                              codes=self.codes_packed)
         y = y.reshape(*lead, self.out_features)
         return y if x.dtype == torch.float16 else y.to(x.dtype)
 
@@ -78,7 +84,7 @@ class Q8Linear(nn.Module):
         buf = scratch.get(kernels.q8_partials_bytes(M, self.in_features, self.out_features), x2.device)
         gen = scratch.generation(x2.device)
         parts, splits = kernels.q8_linear_partials(x2, self.q, self.scales, self.biases, buf, GROUP,
-                                                   packed=self.packed)
+                                                   packed=self.packed, codes=self.codes_packed)
         return ScratchParts(parts, splits, gen)
 
 

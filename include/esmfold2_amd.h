@@ -316,6 +316,29 @@ size_t q8_packed_scales_bytes(int N, int K);
 int q8_pack_scales(const esm_half* s, const esm_half* b, uint32_t* sb, int N, int K, int group, void* stream);
 
 /*
+ * Packs the codes q [N, K] (MLX's layout, one byte per weight) into qp in the order the
+ * GEMM's matrix-core fragments take them: per 160-row tile and step of two groups (128 k),
+ * 4 x 5 chunks of 1 KB, one 16-byte piece per lane; rows past N and groups past K/group
+ * are 0. q8_packed_codes_bytes(N, K) bytes (about N K; 0 for an unsupported shape), qp
+ * 16-byte aligned, q 8-byte aligned. A layout cache of the reference's 8-bit weights
+ * (mlx_esmc.py:53-75), built once per weight matrix like q8_pack_scales. group = 64.
+ */
+size_t q8_packed_codes_bytes(int N, int K);
+int q8_pack_codes(const uint8_t* q, uint8_t* qp, int N, int K, int group, void* stream);
+
+/*
+ * q8_linear_ws and q8_linear_partials on packed weights: qp from q8_pack_codes and sb from
+ * q8_pack_scales of the same matrix (both required; q, s and b are not read). Each wave
+ * loads its matrix-core fragments of the codes straight into registers, so only x and the
+ * scales pass through LDS. Same plan, workspace, partials and results, bit for bit, as the
+ * [N, K] forms; the same reference calls (mlx_esmc.py:78-81).
+ */
+int q8_linear_packed_ws(const esm_half* x, const uint8_t* qp, const uint32_t* sb, esm_half* y, int M, int K, int N,
+                        int group, void* workspace, size_t workspace_bytes, void* stream);
+int q8_linear_packed_partials(const esm_half* x, const uint8_t* qp, const uint32_t* sb, float* parts,
+                              size_t parts_bytes, int* splits, int M, int K, int N, int group, void* stream);
+
+/*
  * The ESMC transformer block's other kernels (mlx_esmc.py:84-102), around q8_linear.
  *
  * esmc_layer_norm: with y, x_out = x + alpha * y (fp32 residual, y fp16: the scaled

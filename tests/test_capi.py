@@ -134,6 +134,33 @@ def test_rejects_null_and_bad_shapes(lib):
     assert lib.tmu_contract(odd, fake, fake, 1, 10, 16, 16, 1.0, None) == -3
 
 
+def test_packed_codes_entry_points_validate(lib):
+    # sizes: per 160-row tile and step of two 64-groups, 4 x 5 chunks of 1 KB
+    assert lib.q8_packed_codes_bytes(160, 128) == 20480
+    assert lib.q8_packed_codes_bytes(161, 192) == 2 * 2 * 20480  # 3 groups -> 2 steps, 2 tiles
+    assert lib.q8_packed_codes_bytes(64, 100) == 0 and lib.q8_packed_codes_bytes(0, 64) == 0
+    assert lib.q8_pack_codes(None, None, 64, 128, 64, None) == -1
+    assert lib.q8_pack_codes(None, None, 64, 128, 32, None) == -4
+    assert lib.q8_pack_codes(None, None, 64, 100, 64, None) == -2
+    assert lib.q8_pack_codes(None, None, 0, 128, 64, None) == 0  # empty: a no-op
+    fake = ctypes.c_void_p(4096)
+    assert lib.q8_pack_codes(ctypes.c_void_p(4096 + 4), fake, 64, 128, 64, None) == -3  # q not 8-byte aligned
+    # the GEMM: packed codes and packed scales are both required; q, s, b are not read
+    assert lib.q8_linear_packed_ws(fake, None, fake, fake, 5, 1024, 64, 64, None, 0, None) == -1
+    assert "packed codes" in _err(lib)
+    assert lib.q8_linear_packed_ws(fake, fake, None, fake, 5, 1024, 64, 64, None, 0, None) == -1
+    assert lib.q8_linear_packed_ws(fake, ctypes.c_void_p(4096 + 8), fake, fake, 5, 1024, 64, 64, None, 0, None) == -3
+    assert lib.q8_linear_packed_ws(fake, fake, fake, fake, 5, 1024, 64, 32, None, 0, None) == -4
+    need = lib.q8_linear_workspace_bytes(5, 1024, 64)
+    assert lib.q8_linear_packed_ws(fake, fake, fake, fake, 5, 1024, 64, 64, ctypes.c_void_p(1 << 20), need - 1,
+                                   None) == -2
+    splits = ctypes.c_int(3)
+    assert lib.q8_linear_packed_partials(fake, fake, fake, fake, 16, ctypes.byref(splits), 5, 1024, 64, 64,
+                                         None) == -2
+    assert splits.value == 0
+    assert lib.q8_linear_packed_partials(fake, fake, fake, fake, 1 << 20, None, 5, 1024, 64, 64, None) == -1
+
+
 def test_pair_forward_validates_before_launching(lib):
     f, ws = ctypes.c_void_p(4096), ctypes.c_void_p(1 << 20)
 

@@ -170,6 +170,66 @@ def test_q8_packed_scales_same_bits(gpu_lib, pkg, M, K, N):
     _check(y_packed.cpu().numpy(), *q8.make_q8_inputs(M, K, N, seed=N))
 
 
+@pytest.mark.parametrize("M,K,N", [(238, 2560, 640), (238, 10240, 320), (238, 5120, 2560), (7, 192, 192),
+                                   (100, 64, 64), (65, 320, 448)])
+def test_q8_packed_codes_same_bits(gpu_lib, pkg, M, K, N):
+    # the packed-code layout is a cache: the same MFMAs in the same order as the [N, K] codes,
+    # so y and the split partials are the same bits; odd group counts (a step's second group
+    # past K), N not a multiple of 160 and split-K shapes included
+    x, q, s, b = (_t(a) for a in q8.make_q8_inputs(M, K, N, seed=N + K))
+    sb = pkg.kernels.q8_pack_scales(s, b)
+    qp = pkg.kernels.q8_pack_codes(q)
+    ws = pkg.kernels.q8_workspace(M, K, N)
+    y_ref = pkg.kernels.q8_linear(x, q, s, b, workspace=ws, packed=sb)
+    y_pc = pkg.kernels.q8_linear(x, q, s, b, workspace=ws, packed=sb, codes=qp)
+    assert torch.equal(y_ref.view(torch.int16), y_pc.view(torch.int16))
+    # without a workspace the tile runs unsplit (another summation order): again equal across layouts
+    y_ref1 = pkg.kernels.q8_linear(x, q, s, b, packed=sb)
+    y_pc1 = pkg.kernels.q8_linear(x, q, s, b, packed=sb, codes=qp)
+    assert torch.equal(y_ref1.view(torch.int16), y_pc1.view(torch.int16))
+    buf_a, buf_b = pkg.kernels.q8_partials_buffer(M, K, N), pkg.kernels.q8_partials_buffer(M, K, N)
+    pa, na = pkg.kernels.q8_linear_partials(x, q, s, b, buf_a, packed=sb)
+    pb, nb = pkg.kernels.q8_linear_partials(x, q, s, b, buf_b, packed=sb, codes=qp)
+    assert na == nb and torch.equal(pa.view(torch.int32), pb.view(torch.int32))
+    if M * K * N <= 238 * 2560 * 640:
+        _check(y_pc.cpu().numpy(), *q8.make_q8_inputs(M, K, N, seed=N + K))
+
+
+def test_q8_packed_codes_layout(gpu_lib, pkg):
+    # chunk ((t S + s) 4 + w) 5 + nb, lane l: row 160 t + 32 nb + l % 32, k = 128 s + 16 w + 8 (l / 32)
+    # + 0..7, then k + 64; zeros past N and past K (N = 200: a partial second tile; 3 groups: the
+    # second step's upper half is past K)
+    N, K = 200, 192
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    qp = pkg.kernels.q8_pack_codes(_t(q)).cpu().numpy()
+    T, S = 2, 2
+    qz = np.zeros((T * 160, S * 128), dtype=np.uint8)
+    qz[:N, :K] = q
+    ref = np.zeros((T, S, 4, 5, 64, 16), dtype=np.uint8)
+    for t in range(T):
+        for st in range(S):
+            for w in range(4):
+                for nb in range(5):
+                    for ln in range(64):
+                        n, k0 = 160 * t + 32 * nb + ln % 32, 128 * st + 16 * w + 8 * (ln // 32)
+                        ref[t, st, w, nb, ln, :8] = qz[n, k0:k0 + 8]
+                        ref[t, st, w, nb, ln, 8:] = qz[n, k0 + 64:k0 + 72]
+    assert np.array_equal(qp, ref.reshape(-1))
+
+
+def test_q8_module_packed_codes_option(gpu_lib, pkg):
+    x, q, s, b = (_t(a) for a in q8.make_q8_inputs(238, 2560, 512, seed=5))
+    on = pkg.q8.Q8Linear(q, s, b, device=DEV)
+    off = pkg.q8.Q8Linear(q, s, b, device=DEV, pack_codes=False)
+    assert on.codes_packed is not None and off.codes_packed is None
+    assert torch.equal(on(x).view(torch.int16), off(x).view(torch.int16))
+    pa, na = on.partials(x)
+    pa = pa.clone()
+    pb, nb = off.partials(x)
+    assert na == nb and torch.equal(pa.view(torch.int32), pb.view(torch.int32))
+
+
 def _quant_cases():
     rng = np.random.default_rng(7)
     w = rng.standard_normal((96, 640)).astype(np.float32) * rng.uniform(0.01, 3, (96, 1)).astype(np.float32)
