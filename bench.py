@@ -75,6 +75,20 @@ def alg_counts(L: int, C: int, c: int):
 
 
 PROFILE_COUNTERS = os.path.join(ROOT, "profiles", "bench_L238_counters.md")
+PROFILE_TRACE = os.path.join(ROOT, "profiles", "bench_L238_kernel_trace.md")
+
+
+def profiled_mean_us(kernel: str, grid: int):
+    """The committed rocprofv3 kernel-trace mean (microseconds) of one kernel at one grid size,
+    from the trace summary's table, or None."""
+    try:
+        for line in open(PROFILE_TRACE):
+            cells = [c.strip() for c in line.split("|")]
+            if len(cells) > 6 and cells[1].strip("`").startswith(kernel) and cells[3] == str(grid):
+                return float(cells[5])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def measured_traffic():
@@ -377,6 +391,15 @@ def main():
                 "per_launch": f"{counts[dom]['bytes'] / 1e6:.2f} MB"}
     roof["duration"] = (f"mean of {kern[dom]['launches']} runtime-stamped kernel durations (hipExtLaunchKernelGGL "
                         "events) over a second pass of the timed step")
+    # the same kernel's mean in the committed kernel trace (another run, possibly another box:
+    # runs scatter by a few per cent, boxes by up to ~10%), and the fraction at that duration
+    grid = {"project": 131072, "contract": 131072, "epilogue": 121856}[dom]  # threads per launch at L=238
+    prof_us = profiled_mean_us("esm::" + kname[dom], grid)
+    if prof_us:
+        per_launch = counts[dom]["flops"] if dom == "contract" else counts[dom]["bytes"]
+        peak = MFMA_F16_PEAK if dom == "contract" else HBM_PEAK
+        roof["profile_us"] = prof_us
+        roof["frac_at_profile_us"] = per_launch / (prof_us * 1e-6) / peak
 
     pair_flops = 2 * sum(v["flops"] for v in counts.values())
     pair_bytes = 2 * sum(v["bytes"] for v in counts.values())
