@@ -66,6 +66,7 @@ SIGNATURES = {
     "q8_pack_codes": (_int, [_vp, _vp, _int, _int, _int, _vp]),
     "q8_linear_packed_ws": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
     "q8_linear_packed_partials": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _int, _int, _int, _int, _vp]),
+    "q8_linear_swiglu_packed_ws": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _sz, _vp]),
     "q8_dequant": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
     "q8_quantize": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
 }

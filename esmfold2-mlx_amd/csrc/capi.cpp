@@ -575,6 +575,34 @@ int q8_linear_packed_ws(const esm_half* x, const uint8_t* qp, const uint32_t* sb
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_packed_ws launch");
 }
 
+int q8_linear_swiglu_packed_ws(const esm_half* x, const uint8_t* qp, const uint32_t* sb, esm_half* y, int M, int K,
+                               int N, int group, void* workspace, size_t workspace_bytes, void* stream) {
+  bool empty;
+  if (!qp) return fail(ESM_ERR_NULL, "q8_linear_swiglu_packed_ws: NULL packed codes");
+  if (const int rc = q8_check_weights("q8_linear_swiglu_packed_ws", x, nullptr, nullptr, nullptr, sb, qp, y, 8, M, K,
+                                      N, group, &empty))
+    return rc;
+  if (empty) return ok();
+  if (N % (2 * esm::kQ8SwigluHalf) != 0)
+    return fail(ESM_ERR_SHAPE, "q8_linear_swiglu_packed_ws: N=%d must be a multiple of %d (SwiGLU pair tiles)", N,
+                2 * esm::kQ8SwigluHalf);
+  Q8Plan pl = q8_plan(M, K, N);
+  if ((long long)pl.mtiles * pl.ntiles * pl.splits > 0x7fffffffLL)
+    return fail(ESM_ERR_SHAPE, "q8_linear_swiglu_packed_ws: M=%d N=%d too large", M, N);
+  if (!workspace) {
+    pl.splits = 1;
+  } else if (pl.splits > 1) {
+    if (workspace_bytes < pl.bytes)
+      return fail(ESM_ERR_SHAPE, "q8_linear_swiglu_packed_ws: workspace of %zu bytes, %zu needed", workspace_bytes,
+                  pl.bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(ESM_ERR_ALIGN, "q8_linear_swiglu_packed_ws: workspace must be 256-byte aligned");
+  }
+  esm::Q8Args a{H(x), nullptr, nullptr, nullptr, H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits,
+                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb, qp, 1};
+  return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_swiglu_packed_ws launch");
+}
+
 int q8_linear_packed_partials(const esm_half* x, const uint8_t* qp, const uint32_t* sb, float* parts,
                               size_t parts_bytes, int* splits, int M, int K, int N, int group, void* stream) {
   bool empty;

@@ -77,6 +77,8 @@ struct Q8Args {
   float* part;          // [splits, M, N] fp32 partials, or nullptr: y written directly (splits 1)
   const uint32_t* sb;   // packed scales [ntiles, K/64, kQ8TileN] (b << 16 | s), or nullptr
   const uint8_t* qp;    // codes packed by q8_pack_codes (needs sb), or nullptr: q is read
+  int swiglu;           // weight rows in SwiGLU pairs (each 160-row tile: 80 gate rows, then the
+                        // matching 80 up rows): y [M, N/2] = silu(gate) * up instead of [M, N]
 };
 
 // q8 GEMM tile: kQ8TileM rows of x by kQ8TileN weight rows, kQ8Waves waves per workgroup.
@@ -200,6 +202,9 @@ hipError_t launch_project(const ProjectArgs& a, int grid, hipStream_t s);
 hipError_t launch_contract(const ContractArgs& a, hipStream_t s);
 hipError_t launch_epilogue(const EpilogueArgs& a, int grid, hipStream_t s);
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s);
+// SwiGLU pair rows: weight row of output column c of a [M, N] product in the pair order,
+// gate f <-> column 160 (f / 80) + f % 80, up f <-> that + 80 (N a multiple of 160).
+constexpr int kQ8SwigluHalf = 80;
 hipError_t launch_transition(const TransitionArgs& a, int grid, hipStream_t s);
 hipError_t launch_esmc_ln(const EsmcLnArgs& a, hipStream_t s);
 hipError_t launch_parcae_step(const ParcaeArgs& a, int grid, hipStream_t s);

@@ -346,6 +346,28 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     for (int w = 1; w < NWQ; w++) v += red[w][blk][r4][lane];
     return v;
   };
+  if (p.part == nullptr && p.swiglu) {
+    // SwiGLU pairs: a lane's 4 gate rows n .. n+3 (n = 32 nb + 8 r4 + 4 h < 80) have their up
+    // rows at n + 80 = 32 (nb + 2) + 8 (r4 + 2) + 4 h: the same lane's sums in block nb + 2 or
+    // nb + 3. Both round to fp16 as y would, then silu(gate) * up in fp32 as esmc_swiglu does.
+    constexpr int HALF = kQ8SwigluHalf, NG = MBQ * HALF / 8;  // gate groups of 8 rows per tile
+    const int F = N / 2;
+    for (int gi = wave; gi < NG; gi += NWQ) {
+      const int mb = gi / (HALF / 8), g8 = gi - mb * (HALF / 8);  // gate rows 8 g8 .. 8 g8 + 7
+      const int nb = g8 >> 2, r4 = g8 & 3;
+      const int ru = r4 + 2, nbu = nb + 2 + (ru >> 2);
+      const f32x4 g = tile_sum(mb * NBQ + nb, r4), u = tile_sum(mb * NBQ + nbu, ru & 3);
+      const int m = m0 + 32 * mb + r, f = nt * HALF + 8 * g8 + 4 * kg;
+      half4 o;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float a = (float)(half_t)g[e];
+        o[e] = (half_t)(a * sigmoidf_fast(a) * (float)(half_t)u[e]);
+      }
+      if (m < M && f < F) *reinterpret_cast<half4*>(p.y + (size_t)m * F + f) = o;
+    }
+    return;
+  }
   if (p.part == nullptr) {  // one K range per tile: fp16 y directly
     for (int blk = wave; blk < NBLK; blk += NWQ) {
       const int mb = blk / NBQ, nb = blk - mb * NBQ;
@@ -384,6 +406,32 @@ __global__ __launch_bounds__(256) void q8_reduce_kernel(const float* __restrict_
     f32x4 v = reinterpret_cast<const f32x4*>(part)[i];
     for (int s = 1; s < splits; s++) v += reinterpret_cast<const f32x4*>(part + (size_t)s * plane)[i];
     reinterpret_cast<half4*>(y)[i] = half4{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+  }
+}
+
+// The same for SwiGLU pair rows: out [M, F] = silu(gate) * up, each of gate and up summed over
+// the splits in order and rounded to fp16 first (the bits of the fused epilogue). Four outputs
+// per thread; F is a multiple of 80.
+__global__ __launch_bounds__(256) void q8_reduce_swiglu_kernel(const float* __restrict__ part,
+                                                               half_t* __restrict__ y, int M, int F, int splits) {
+  const size_t plane = (size_t)M * 2 * F, n4 = (size_t)M * F / 4;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t m = 4 * i / F;
+    const int f = (int)(4 * i - m * F);
+    const int cg = 2 * kQ8SwigluHalf * (f / kQ8SwigluHalf) + f % kQ8SwigluHalf;  // gate column
+    const float* pg = part + m * 2 * F + cg;
+    f32x4 g = *reinterpret_cast<const f32x4*>(pg), u = *reinterpret_cast<const f32x4*>(pg + kQ8SwigluHalf);
+    for (int s = 1; s < splits; s++) {
+      g += *reinterpret_cast<const f32x4*>(pg + s * plane);
+      u += *reinterpret_cast<const f32x4*>(pg + s * plane + kQ8SwigluHalf);
+    }
+    half4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float a = (float)(half_t)g[e];
+      o[e] = (half_t)(a * sigmoidf_fast(a) * (float)(half_t)u[e]);
+    }
+    *reinterpret_cast<half4*>(y + 4 * i) = o;
   }
 }
 
@@ -497,7 +545,11 @@ hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s) {
     ESM_LAUNCH((q8_linear_kernel<true, false>), dim3(grid), dim3(NWQ * 64), 0, s, a);
   else
     ESM_LAUNCH((q8_linear_kernel<false, false>), dim3(grid), dim3(NWQ * 64), 0, s, a);
-  if (a.part && a.y) {  // partials and an fp16 output: sum them here (no y: the caller's consumer does)
+  if (a.part && a.y && a.swiglu) {  // partials of SwiGLU pair rows: summed and gated here
+    const size_t n4 = (size_t)a.M * (a.N / 2) / 4, blocks = (n4 + 255) / 256;
+    ESM_LAUNCH(q8_reduce_swiglu_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, s, a.part, a.y,
+               a.M, a.N / 2, a.splits);
+  } else if (a.part && a.y) {  // partials and an fp16 output: sum them here (no y: the caller's consumer does)
     const size_t plane = (size_t)a.M * a.N, n4 = plane / 4;
     const size_t blocks = (n4 + 255) / 256;
     ESM_LAUNCH(q8_reduce_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, s, a.part, a.y,

@@ -67,6 +67,8 @@ class EsmcBlock(nn.Module):
                      ("ln2_b", ln2_b)):
             self.register_buffer(n, f(t))
         self.wqkv, self.wo, self.w1, self.w2 = wqkv, wo, w1, w2
+        if w1.out_features % (2 * kernels.SWIGLU_HALF) == 0:
+            w1.swiglu_pairs()  # the FFN's SwiGLU runs inside w1's GEMM
         self.D = wo.out_features
         self.F = w2.in_features
         self.n_heads = n_heads
@@ -115,7 +117,8 @@ class EsmcBlock(nn.Module):
     def ffn(self, h2: torch.Tensor):
         """w2(silu(x1) * x2) with [x1 | x2] = w1(h2) (before the residual's / res_scale), as w2's
         split-K partials: (partials, splits) for ``esmc_layer_norm(..., y_parts=...)``."""
-        return self.w2.partials(kernels.esmc_swiglu(self.w1(h2)))
+        act = self.w1.swiglu(h2) if self.w1.pair_rows else kernels.esmc_swiglu(self.w1(h2))
+        return self.w2.partials(act)
 
     def forward(self, x: torch.Tensor, sequence_id=None, res_scale: float = 1.0) -> torch.Tensor:
         """One block on an fp32 residual [B, L, D] (the reference's block_forward, mlx_esmc.py:84-102)."""

@@ -344,6 +344,43 @@ def q8_pack_codes(q, group: int = 64):
     return qp
 
 
+SWIGLU_HALF = 80  # gate (or up) rows per 160-row tile in the SwiGLU pair order
+
+
+def swiglu_pair_rows(N: int, device=None):
+    """Row order of a [gate; up] weight [N, K] (N = 2F, a multiple of 160) in which each 160-row
+    tile holds gate rows 80 t .. 80 t + 79 and then up rows F + 80 t .. F + 80 t + 79."""
+    if N % (2 * SWIGLU_HALF):
+        raise capi.EsmError(-2, f"swiglu_pair_rows: N={N} must be a multiple of {2 * SWIGLU_HALF}")
+    F = N // 2
+    t = torch.arange(N // (2 * SWIGLU_HALF)).view(-1, 1) * SWIGLU_HALF
+    j = torch.arange(SWIGLU_HALF).view(1, -1)
+    return torch.cat([t + j, F + t + j], dim=1).reshape(-1).to(device if device is not None else "cpu")
+
+
+def q8_linear_swiglu(x, codes, packed, N: int, group: int = 64, out=None, workspace=None):
+    """silu(x W_gate^T) * (x W_up^T) [M, N/2] from the [gate; up] weight packed in SwiGLU pair
+    order (``q8_pack_codes`` / ``q8_pack_scales`` of its rows taken in ``swiglu_pair_rows(N)``):
+    the same bits as ``esmc_swiglu(q8_linear(x, ...))`` on the [gate; up] rows."""
+    lib = capi.lib()
+    _dev(x, "x", F16)
+    _dev(packed, "packed", torch.int32)
+    M, K = x.shape
+    qp = _packed_codes(lib, "q8_linear_swiglu", codes, packed, N, K)
+    if packed.numel() * 4 < lib.q8_packed_scales_bytes(N, K):
+        raise capi.EsmError(-2, "q8_linear_swiglu: packed scales too small for this shape")
+    y = torch.empty(M, N // 2, dtype=F16, device=x.device) if out is None else _out(out, "out", F16, M * (N // 2))
+    if workspace is None:
+        wp, wn = None, 0
+    else:
+        _dev(workspace, "workspace", torch.uint8)
+        wp = (workspace.data_ptr() + 255) // 256 * 256
+        wn = workspace.numel() - (wp - workspace.data_ptr())
+    capi.check(lib.q8_linear_swiglu_packed_ws(x.data_ptr(), qp, packed.data_ptr(), y.data_ptr(), M, K, N, group,
+                                              wp, wn, capi.stream_ptr()))
+    return y
+
+
 def q8_linear(x, q, s, b, group: int = 64, out=None, workspace=None, packed=None, codes=None):
     """Kernel (d): y = x . W^T, W = s*q + b per group of 64 along K (fp16 in/out, fp32 accumulation).
     ``packed`` (from ``q8_pack_scales``), ``codes`` (from ``q8_pack_codes``, used with ``packed``) and

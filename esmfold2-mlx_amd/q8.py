@@ -39,6 +39,35 @@ class Q8Linear(nn.Module):
         self.in_features, self.out_features = K, N
         self.register_buffer("packed", kernels.q8_pack_scales(self.scales, self.biases, GROUP))
         self.register_buffer("codes_packed", kernels.q8_pack_codes(self.q, GROUP) if pack_codes else None)
+        self.pair_rows = False  # packed layouts in SwiGLU pair order (``swiglu_pairs``)
+
+    def swiglu_pairs(self) -> "Q8Linear":
+        """Re-packs a [gate; up] linear (the ESMC block's w1) in SwiGLU pair order for ``swiglu``,
+        which then gates inside the GEMM; ``forward`` and ``partials`` keep their results and read
+        the [N, K] arrays. Returns self."""
+        if not self.pair_rows:
+            perm = kernels.swiglu_pair_rows(self.out_features, self.q.device)
+            self.packed = kernels.q8_pack_scales(self.scales[perm].contiguous(), self.biases[perm].contiguous(), GROUP)
+            self.codes_packed = kernels.q8_pack_codes(self.q[perm].contiguous(), GROUP)
+            self.pair_rows = True
+        return self
+
+    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
+        """silu(x W_gate^T) * (x W_up^T), [..., out_features / 2] fp16: the same bits as
+        ``kernels.esmc_swiglu(self(x))`` (needs ``swiglu_pairs``)."""
+        if not self.pair_rows:
+            raise ValueError("Q8Linear.swiglu needs swiglu_pairs() first")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
+        M = x2.shape[0]
+        n = kernels.q8_workspace_bytes(M, self.in_features, self.out_features)
+        ws = scratch.get(n, x2.device) if n else None
+        y = kernels.q8_linear_swiglu(x2, self.codes_packed, self.packed, self.out_features, GROUP, workspace=ws)
+        return y.reshape(*lead, self.out_features // 2)
+
+    def _layouts(self):
+        """(packed scales, packed codes) for the plain product: none once re-packed in pair order."""
+        return (None, None) if self.pair_rows else (self.packed, self.codes_packed)
 
     @classmethod
     def from_float(cls, w: torch.Tensor, **kw) -> "Q8Linear":
@@ -67,8 +96,8 @@ class Q8Linear(nn.Module):
         M = x2.shape[0]
         n = kernels.q8_workspace_bytes(M, self.in_features, self.out_features)
         ws = scratch.get(n, x2.device) if n else None  # split-K partials, only while this call runs
-        y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP, workspace=ws, packed=self.packed,
-                              codes=self.codes_packed)
+        sb, qp = self._layouts()
+        y = kernels.q8_linear(x2, self.q, self.scales, self.biases, GROUP, workspace=ws, packed=sb, codes=qp)
         y = y.reshape(*lead, self.out_features)
         return y if x.dtype == torch.float16 else y.to(x.dtype)
 
@@ -83,8 +112,9 @@ class Q8Linear(nn.Module):
         M = x2.shape[0]
         buf = scratch.get(kernels.q8_partials_bytes(M, self.in_features, self.out_features), x2.device)
         gen = scratch.generation(x2.device)
-        parts, splits = kernels.q8_linear_partials(x2, self.q, self.scales, self.biases, buf, GROUP,
-                                                   packed=self.packed, codes=self.codes_packed)
+        sb, qp = self._layouts()
+        parts, splits = kernels.q8_linear_partials(x2, self.q, self.scales, self.biases, buf, GROUP, packed=sb,
+                                                   codes=qp)
         return ScratchParts(parts, splits, gen)
 
 

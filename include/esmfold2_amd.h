@@ -339,6 +339,18 @@ int q8_linear_packed_partials(const esm_half* x, const uint8_t* qp, const uint32
                               size_t parts_bytes, int* splits, int M, int K, int N, int group, void* stream);
 
 /*
+ * The block's first FFN linear and its SwiGLU in one call: y [M, N/2] = silu(x W_gate^T) *
+ * (x W_up^T), W = [gate; up] rows [N, K] (mlx_esmc.py:100-101, the `w1` linear then
+ * silu(x1) * x2). qp and sb are q8_pack_codes / q8_pack_scales of the rows in SwiGLU pair
+ * order: each 160-row tile holds gate rows 80 t .. 80 t + 79, then up rows 80 t .. 80 t + 79
+ * (N a multiple of 160). Same bits as q8_linear_ws on the [gate; up] rows followed by
+ * esmc_swiglu: the gate and up sums round to fp16 before the gating, unsplit in the GEMM's
+ * epilogue, split-K in the reduction of the partials (workspace as for q8_linear_ws at M, K, N).
+ */
+int q8_linear_swiglu_packed_ws(const esm_half* x, const uint8_t* qp, const uint32_t* sb, esm_half* y, int M, int K,
+                               int N, int group, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * The ESMC transformer block's other kernels (mlx_esmc.py:84-102), around q8_linear.
  *
  * esmc_layer_norm: with y, x_out = x + alpha * y (fp32 residual, y fp16: the scaled

@@ -161,6 +161,18 @@ def test_packed_codes_entry_points_validate(lib):
     assert lib.q8_linear_packed_partials(fake, fake, fake, fake, 1 << 20, None, 5, 1024, 64, 64, None) == -1
 
 
+def test_swiglu_pair_rows_and_checks(pkg, lib):
+    perm = pkg.kernels.swiglu_pair_rows(320)
+    # tile 0: gate rows 0..79 then up rows 160..239; tile 1: gate 80..159 then up 240..319
+    assert perm[:80].tolist() == list(range(80)) and perm[80:160].tolist() == list(range(160, 240))
+    assert perm[160:240].tolist() == list(range(80, 160)) and perm[240:].tolist() == list(range(240, 320))
+    assert sorted(perm.tolist()) == list(range(320))
+    fake = ctypes.c_void_p(4096)
+    assert lib.q8_linear_swiglu_packed_ws(fake, None, fake, fake, 5, 128, 320, 64, None, 0, None) == -1
+    assert lib.q8_linear_swiglu_packed_ws(fake, fake, fake, fake, 5, 128, 192, 64, None, 0, None) == -2
+    assert "multiple of 160" in _err(lib)
+
+
 def test_pair_forward_validates_before_launching(lib):
     f, ws = ctypes.c_void_p(4096), ctypes.c_void_p(1 << 20)
 

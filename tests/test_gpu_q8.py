@@ -218,6 +218,41 @@ def test_q8_packed_codes_layout(gpu_lib, pkg):
     assert np.array_equal(qp, ref.reshape(-1))
 
 
+@pytest.mark.parametrize("M,K,N", [(238, 2560, 10240), (50, 2560, 10240), (7, 192, 320), (100, 640, 640)])
+def test_q8_swiglu_fused_same_bits(gpu_lib, pkg, M, K, N):
+    # w1 then SwiGLU in one call (rows in SwiGLU pair order) against the two calls on [gate; up]:
+    # unsplit (the GEMM's epilogue gates) and split-K (the reduction gates), same bits
+    K_ = pkg.kernels
+    x, q, s, b = (_t(a) for a in q8.make_q8_inputs(M, K, N, seed=M + N))
+    ws = K_.q8_workspace(M, K, N)
+    ref = K_.esmc_swiglu(K_.q8_linear(x, q, s, b, workspace=ws))
+    perm = K_.swiglu_pair_rows(N, DEV)
+    sbp = K_.q8_pack_scales(s[perm].contiguous(), b[perm].contiguous())
+    qpp = K_.q8_pack_codes(q[perm].contiguous())
+    got = K_.q8_linear_swiglu(x, qpp, sbp, N, workspace=ws)
+    assert got.shape == (M, N // 2)
+    assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
+    got1 = K_.q8_linear_swiglu(x, qpp, sbp, N)  # no workspace: unsplit
+    ref1 = K_.esmc_swiglu(K_.q8_linear(x, q, s, b))
+    assert torch.equal(ref1.view(torch.int16), got1.view(torch.int16))
+    # and against the fp64 oracle of silu(x W_g) * (x W_u)
+    xs, qs, ss, bs = q8.make_q8_inputs(M, K, N, seed=M + N)
+    y = q8.q8_linear(xs, qs, ss, bs)
+    g, u = y[:, :N // 2], y[:, N // 2:]
+    want = g / (1 + np.exp(-g)) * u
+    rel = np.linalg.norm(got.cpu().numpy().astype(np.float64) - want) / np.linalg.norm(want)
+    assert rel <= 3e-3, f"normwise relative error {rel:.3e}"  # the GEMM's ~3e-4 and two fp16 roundings
+
+
+def test_q8_module_swiglu_pairs(gpu_lib, pkg):
+    x, q, s, b = (_t(a) for a in q8.make_q8_inputs(238, 640, 1280, seed=9))
+    lin = pkg.q8.Q8Linear(q, s, b, device=DEV)
+    y0 = lin(x)
+    lin.swiglu_pairs()
+    assert torch.equal(lin(x).view(torch.int16), y0.view(torch.int16))  # forward unchanged
+    assert torch.equal(lin.swiglu(x).view(torch.int16), pkg.kernels.esmc_swiglu(y0).view(torch.int16))
+
+
 def test_q8_module_packed_codes_option(gpu_lib, pkg):
     x, q, s, b = (_t(a) for a in q8.make_q8_inputs(238, 2560, 512, seed=5))
     on = pkg.q8.Q8Linear(q, s, b, device=DEV)
