@@ -50,64 +50,94 @@ DEV float2v wg_sum2(float a, float b, float (*red)[4]) {
 }
 
 // ---- residual + LayerNorm -------------------------------------------------------------------
+// Thread t holds the element groups i = 4 (t + 256 j), j < NJ = ceil(D / 1024). Every load is
+// a range-checked buffer load (groups past D load zeros and are masked out of the sums) issued
+// before the first use, and the split count of the common plans is a template parameter, so
+// a row's x and all of its split partials are in flight together: with a branch around each
+// group and a loop over the splits every partial waited for the one before it. The sums keep
+// their order (splits in order, rounded once to fp16, then the residual; groups in order for
+// the statistics).
+template <int NJ, int NSPL>  // NSPL: y's split partials, a fixed count (unrolled) or -1 (any count)
 __global__ __launch_bounds__(NTR) void esmc_ln_kernel(EsmcLnArgs p) {
   __shared__ float red[4];
-  const int row = blockIdx.x, D = p.D;
-  const float* x = p.x + (size_t)row * D;
-  float* xo = p.x_out + (size_t)row * D;
-  const half_t* y = p.y ? p.y + (size_t)row * D : nullptr;
-  const float* yp = p.yp ? p.yp + (size_t)row * D : nullptr;
-  const size_t plane = (size_t)p.M * D;
-  half_t* h = p.h ? p.h + (size_t)row * D : nullptr;
-  float* h32 = p.h32 ? p.h32 + (size_t)row * D : nullptr;
-  constexpr int MAXV = 8;  // D <= 8 * 4 * 256
-  f32x4 v[MAXV];
+  const int row = blockIdx.x, D = p.D, t = threadIdx.x;
+  const uint32_t rowb = (uint32_t)D * 4u;
+  auto off = [&](int j) { return (uint32_t)(4 * (t + NTR * j)) * 4u; };  // bytes into an fp32 row
+  auto valid = [&](int j) { return 4 * (t + NTR * j) < D; };
+  auto ld4 = [&](rsrc_t r, int j) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off(j), 0, 0)); };
+  const rsrc_t rx = make_rsrc_n(p.x + (size_t)row * D, rowb);
+  f32x4 v[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) v[j] = ld4(rx, j);
+  const bool res = p.y || p.yp;
+  if (p.yp) {
+    const size_t plane = (size_t)p.M * D;
+    auto part = [&](int sp) { return make_rsrc_n(p.yp + sp * plane + (size_t)row * D, rowb); };
+    f32x4 a[NJ];
+    if constexpr (NSPL > 0) {  // every partial in flight at once
+      f32x4 l[NSPL][NJ];
+#pragma unroll
+      for (int sp = 0; sp < NSPL; sp++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) l[sp][j] = ld4(part(sp), j);
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        a[j] = l[0][j];
+#pragma unroll
+        for (int sp = 1; sp < NSPL; sp++) a[j] += l[sp][j];
+      }
+    } else {  // any count: one split's groups in flight at a time
+#pragma unroll
+      for (int j = 0; j < NJ; j++) a[j] = ld4(part(0), j);
+      for (int sp = 1; sp < p.splits; sp++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) a[j] += ld4(part(sp), j);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[j][e] += p.alpha * (float)(half_t)a[j][e];
+  } else if (p.y) {
+    const rsrc_t ry = make_rsrc_n(p.y + (size_t)row * D, (uint32_t)D * 2u);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const half4 yy = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(ry, (int)(off(j) / 2), 0, 0));
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[j][e] += p.alpha * (float)yy[e];
+    }
+  }
+  const rsrc_t rxo = make_rsrc_n(p.x_out + (size_t)row * D, res ? rowb : 0u);
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < MAXV; j++) {
-    const int i = 4 * (threadIdx.x + NTR * j);
-    if (i < D) {
-      f32x4 t = *reinterpret_cast<const f32x4*>(x + i);
-      if (y || yp) {
-        half4 yy;
-        if (yp) {  // the linear's split partials, summed in split order and rounded once (as q8_reduce_kernel)
-          f32x4 a = *reinterpret_cast<const f32x4*>(yp + i);
-          for (int sp = 1; sp < p.splits; sp++) a += *reinterpret_cast<const f32x4*>(yp + sp * plane + i);
-          yy = half4{(half_t)a[0], (half_t)a[1], (half_t)a[2], (half_t)a[3]};
-        } else {
-          yy = *reinterpret_cast<const half4*>(y + i);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) t[e] += p.alpha * (float)yy[e];
-        *reinterpret_cast<f32x4*>(xo + i) = t;
-      }
-      v[j] = t;
-      s += t[0] + t[1] + t[2] + t[3];
-    }
+  for (int j = 0; j < NJ; j++) {
+    if (res) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[j]), rxo, (int)off(j), 0, 0);
+    const float sj = s + (v[j][0] + v[j][1] + v[j][2] + v[j][3]);
+    s = valid(j) ? sj : s;
   }
   const float mean = wg_sum(s, red) / D;
   float q = 0.f;
 #pragma unroll
-  for (int j = 0; j < MAXV; j++) {
-    const int i = 4 * (threadIdx.x + NTR * j);
-    if (i < D)
+  for (int j = 0; j < NJ; j++) {
+    float qj = q;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        v[j][e] -= mean;
-        q += v[j][e] * v[j][e];
-      }
+    for (int e = 0; e < 4; e++) {
+      v[j][e] -= mean;
+      qj += v[j][e] * v[j][e];
+    }
+    q = valid(j) ? qj : q;
   }
   const float rstd = rsqrtf(wg_sum(q, red) / D + p.eps);
+  const rsrc_t rw = make_rsrc_n(p.w, rowb), rb = make_rsrc_n(p.b ? (const void*)p.b : (const void*)p.w, p.b ? rowb : 0u);
+  const rsrc_t rh = make_rsrc_n(p.h ? (void*)(p.h + (size_t)row * D) : (void*)p.w, p.h ? (uint32_t)D * 2u : 0u);
+  const rsrc_t rh32 = make_rsrc_n(p.h32 ? (void*)(p.h32 + (size_t)row * D) : (void*)p.w, p.h32 ? rowb : 0u);
 #pragma unroll
-  for (int j = 0; j < MAXV; j++) {
-    const int i = 4 * (threadIdx.x + NTR * j);
-    if (i < D) {
-      f32x4 o;
+  for (int j = 0; j < NJ; j++) {
+    const f32x4 w4 = ld4(rw, j), b4 = ld4(rb, j);  // (no bias: zeros)
+    f32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; e++) o[e] = v[j][e] * rstd * p.w[i + e] + (p.b ? p.b[i + e] : 0.f);
-      if (h) *reinterpret_cast<half4*>(h + i) = half4{(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
-      if (h32) *reinterpret_cast<f32x4*>(h32 + i) = o;
-    }
+    for (int e = 0; e < 4; e++) o[e] = v[j][e] * rstd * w4[e] + b4[e];
+    if (p.h) bstore8(rh, off(j) / 2, half4{(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]});
+    if (p.h32) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), rh32, (int)off(j), 0, 0);
   }
 }
 
@@ -410,9 +440,32 @@ __global__ __launch_bounds__(256) void esmc_swiglu_kernel(const half_t* __restri
   }
 }
 
-hipError_t launch_esmc_ln(const EsmcLnArgs& a, hipStream_t s) {
-  ESM_LAUNCH(esmc_ln_kernel, dim3(a.M), dim3(NTR), 0, s, a);
+template <int NJ>
+static hipError_t launch_esmc_ln_nj(const EsmcLnArgs& a, hipStream_t s) {
+  const int ns = a.yp ? a.splits : 0;
+  if (ns == 4)
+    ESM_LAUNCH((esmc_ln_kernel<NJ, 4>), dim3(a.M), dim3(NTR), 0, s, a);
+  else if (ns == 2)
+    ESM_LAUNCH((esmc_ln_kernel<NJ, 2>), dim3(a.M), dim3(NTR), 0, s, a);
+  else if (ns == 1)
+    ESM_LAUNCH((esmc_ln_kernel<NJ, 1>), dim3(a.M), dim3(NTR), 0, s, a);
+  else  // no partials (NSPL is then unused), or another count
+    ESM_LAUNCH((esmc_ln_kernel<NJ, -1>), dim3(a.M), dim3(NTR), 0, s, a);
   return hipGetLastError();
+}
+
+hipError_t launch_esmc_ln(const EsmcLnArgs& a, hipStream_t s) {
+  switch ((a.D + 4 * NTR - 1) / (4 * NTR)) {  // element groups per thread
+    case 1: return launch_esmc_ln_nj<1>(a, s);
+    case 2: return launch_esmc_ln_nj<2>(a, s);
+    case 3: return launch_esmc_ln_nj<3>(a, s);
+    case 4: return launch_esmc_ln_nj<4>(a, s);
+    case 5: return launch_esmc_ln_nj<5>(a, s);
+    case 6: return launch_esmc_ln_nj<6>(a, s);
+    case 7: return launch_esmc_ln_nj<7>(a, s);
+    case 8: return launch_esmc_ln_nj<8>(a, s);
+    default: return hipErrorInvalidValue;  // D <= 8192 is checked by the caller
+  }
 }
 
 hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s) {
