@@ -31,9 +31,10 @@ Also reported on the same JSON line:
                 distogram expected distance (64 bins) and the p95 exit quantile;
   esmc_block    one ESMC transformer block at 238 tokens, D=2560, 40 heads, FFN 5120
                 (its wqkv, wo, w1, w2 8-bit linears and the LN / RoPE / attention /
-                SwiGLU kernels) replayed as one HIP graph, every replay checked
-                against the eager output; the eager time, bound by the 13 host
-                launches, beside it;
+                SwiGLU kernels) as one HIP graph: 20 back-to-back replays timed,
+                replays checked against the eager output (three with eager
+                launches in between, and the last timed one); the eager time,
+                bound by the host launches, beside it;
   pair_c256     the same TMU pair at ESMFold2's real width, C = c = 256 (the wide path);
   cpu_baseline  the CPU oracle (torch fp32 restatement of the reference's
                 _trimul_forward) on the host cores, a bounded sample of the same
@@ -621,16 +622,20 @@ def main():
             yg = blk(xed, None, res_scale=rs)
         held = pkg.scratch.current(dev)  # the shared scratch the captured launches use stays alive
         replays_equal = True
-        ts = []
-        for _ in range(5):
-            e0.record(stream)
+        for _ in range(3):  # each replay checked against the eager output, eager launches in between
             g.replay()
-            e1.record(stream)
             torch.cuda.synchronize()
-            ts.append(e0.elapsed_time(e1) * 1e-3)
             replays_equal &= bool(torch.equal(yg, ye))
             blk(xed, None, res_scale=rs)
-        t = statistics.median(ts)
+        torch.cuda.synchronize()
+        reps = 20  # timed: back-to-back replays, the block's steady-state time
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        replays_equal &= bool(torch.equal(yg, ye))
         fl = 2 * L * ED * (3 * ED + ED + 2 * EF + EF) + 4 * L * L * ED  # linears + attention
         wbytes = sum(q.numel() + 4 * s_.numel() for q, s_, _ in lin.values())
         out["esmc_block"] = {"us": t * 1e6, "eager_us": t_eager * 1e6, "tokens": L, "D": ED, "ffn": EF,

@@ -754,8 +754,8 @@ int esmc_qk_rope(const esm_half* qkv, const float* q_ln, const float* k_ln, floa
   if (!(eps >= 0.f)) return fail(ESM_ERR_SHAPE, "esmc_qk_rope: eps must be >= 0");
   if (B == 0 || L == 0) return ok();
   if (!qkv || !q_ln || !k_ln || !q || !k || !v) return fail(ESM_ERR_NULL, "esmc_qk_rope: NULL pointer");
-  if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || !aligned16(v))
-    return fail(ESM_ERR_ALIGN, "esmc_qk_rope: qkv, q, k, v must be 16-byte aligned");
+  if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(q_ln) || !aligned16(k_ln))
+    return fail(ESM_ERR_ALIGN, "esmc_qk_rope: qkv, q_ln, k_ln, q, k, v must be 16-byte aligned");
   esm::EsmcRopeArgs a{H(qkv), q_ln, k_ln, eps, H(q), H(k), H(v), B, L, n_heads, std::log2(rope_base)};
   return hip_status(esm::launch_esmc_qk_rope(a, (hipStream_t)stream), "esmc_qk_rope launch");
 }

@@ -145,12 +145,51 @@ __global__ __launch_bounds__(NTR) void esmc_ln_kernel(EsmcLnArgs p) {
 // Thread -> chunks of 8 rotation pairs: chunk u < D/16 of q, else of k (u' = u mod D/16);
 // pairs (e, e + 32) of head u' / 4 at e = 8 (u' % 4) .. + 7, so a chunk is two 16-byte
 // loads and two 16-byte stores. The LayerNorm statistics of q and k are reduced together.
+// Every load is issued first (v's chunks, then the q/k chunks through a range-checked
+// descriptor of the row, then their LayerNorm weights), and v leaves as soon as it has
+// arrived, so the row's memory latencies overlap instead of following one another.
 __global__ __launch_bounds__(NTR) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
   __shared__ float red[2][4];
-  constexpr int HD = 64, HALF = 32, MAXC = 2;  // 2 * D / 16 <= MAXC * NTR for D <= 4096
+  constexpr int HD = 64, HALF = 32, MAXC = 2, MAXV = 2;  // 2 D / 16 and D / 8 <= MAXC * NTR for D <= 4096
   const int row = blockIdx.x, D = p.H * HD, nq = D / 16;
   const int b = row / p.L, l = row - b * p.L;
   const half_t* src = p.qkv + (size_t)row * 3 * D;
+  const rsrc_t rs = make_rsrc_n(src, (uint32_t)(3 * D) * 2u);
+  half8 vv[MAXV], x1[MAXC], x2[MAXC];
+  f32x4 wl[MAXC][4];
+#pragma unroll
+  for (int k = 0; k < MAXV; k++) {
+    const int e = 8 * (threadIdx.x + NTR * k);
+    vv[k] = bload16(rs, e < D ? (uint32_t)(2 * D + e) * 2u : kOOB);
+  }
+#pragma unroll
+  for (int j = 0; j < MAXC; j++) {
+    const int u = threadIdx.x + NTR * j;
+    const bool ok = u < 2 * nq;
+    const int which = u >= nq, uu = u - which * nq;
+    const uint32_t off = (uint32_t)(which * D + (uu >> 2) * HD + 8 * (uu & 3)) * 2u;
+    x1[j] = bload16(rs, ok ? off : kOOB);
+    x2[j] = bload16(rs, ok ? off + 2u * HALF : kOOB);
+  }
+#pragma unroll
+  for (int j = 0; j < MAXC; j++) {
+    const int u = threadIdx.x + NTR * j;
+    const int which = u >= nq, uu = u - which * nq;
+    const float* w = u < 2 * nq ? (which ? p.k_ln : p.q_ln) + (uu >> 2) * HD + 8 * (uu & 3) : p.q_ln;
+    wl[j][0] = *reinterpret_cast<const f32x4*>(w);
+    wl[j][1] = *reinterpret_cast<const f32x4*>(w + 4);
+    wl[j][2] = *reinterpret_cast<const f32x4*>(w + HALF);
+    wl[j][3] = *reinterpret_cast<const f32x4*>(w + HALF + 4);
+  }
+  // v: head-major, 8 halfs per thread
+#pragma unroll
+  for (int k = 0; k < MAXV; k++) {
+    const int e = 8 * (threadIdx.x + NTR * k);
+    if (e < D) {
+      const int hh = e / HD, d = e % HD;
+      st16(p.v + (((size_t)b * p.H + hh) * p.L + l) * HD + d, vv[k]);
+    }
+  }
   float a[MAXC][8], c[MAXC][8], sq = 0.f, sk = 0.f;
 #pragma unroll
   for (int j = 0; j < MAXC; j++) {
@@ -158,14 +197,12 @@ __global__ __launch_bounds__(NTR) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
 #pragma unroll
     for (int e = 0; e < 8; e++) a[j][e] = c[j][e] = 0.f;
     if (u < 2 * nq) {
-      const int which = u >= nq, uu = u - which * nq;
-      const half_t* v = src + which * D + (uu >> 2) * HD + 8 * (uu & 3);
-      const half8 x1 = ld16(v), x2 = ld16(v + HALF);
+      const int which = u >= nq;
       float t = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        a[j][e] = (float)x1[e];
-        c[j][e] = (float)x2[e];
+        a[j][e] = (float)x1[j][e];
+        c[j][e] = (float)x2[j][e];
         t += a[j][e] + c[j][e];
       }
       sq += which ? 0.f : t;
@@ -198,7 +235,6 @@ __global__ __launch_bounds__(NTR) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
     const int u = threadIdx.x + NTR * j;
     if (u < 2 * nq) {
       const int which = u >= nq, uu = u - which * nq, hh = uu >> 2, i0 = 8 * (uu & 3);
-      const float* w = (which ? p.k_ln : p.q_ln) + hh * HD;
       const float rstd = which ? rk : rq;
       half8 o1, o2;
 #pragma unroll
@@ -208,19 +244,14 @@ __global__ __launch_bounds__(NTR) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
         const float ang = (float)l * exp2f(-(float)(2 * i) / HD * p.log2_base);
         float sn, cs;
         sincosf(ang, &sn, &cs);
-        const float x1 = a[j][e] * rstd * w[i], x2 = c[j][e] * rstd * w[i + HALF];
-        o1[e] = (half_t)(x1 * cs - x2 * sn);
-        o2[e] = (half_t)(x2 * cs + x1 * sn);
+        const float x1v = a[j][e] * rstd * wl[j][e >> 2][e & 3], x2v = c[j][e] * rstd * wl[j][2 + (e >> 2)][e & 3];
+        o1[e] = (half_t)(x1v * cs - x2v * sn);
+        o2[e] = (half_t)(x2v * cs + x1v * sn);
       }
       half_t* o = (which ? p.k : p.q) + (((size_t)b * p.H + hh) * p.L + l) * HD + i0;
       st16(o, o1);
       st16(o + HALF, o2);
     }
-  }
-  // v: copy to head-major, 8 halfs per thread
-  for (int c8 = threadIdx.x; c8 < D / 8; c8 += NTR) {
-    const int e = 8 * c8, hh = e / HD, d = e % HD;
-    st16(p.v + (((size_t)b * p.H + hh) * p.L + l) * HD + d, ld16(src + 2 * D + e));
   }
 }
 

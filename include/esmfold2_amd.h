@@ -363,7 +363,7 @@ int q8_linear_swiglu_packed_ws(const esm_half* x, const uint8_t* qp, const uint3
  *   over the full width D with weights only (:93-94), fp32 statistics; NeoX rotary
  *   embedding (mx.fast.rope traditional=False, base rope_base, positions 0..L-1,
  *   :96-97); q, k, v written head-major [B, H, L, 64] fp16. head_dim = 64, D <= 4096;
- *   qkv, q, k, v 16-byte aligned.
+ *   qkv, q_ln, k_ln, q, k, v 16-byte aligned.
  * esmc_attention: o = softmax(q k^T * scale, mask) v per (batch, head) (:98,
  *   mx.fast.scaled_dot_product_attention), with token i attending to j iff
  *   sequence_id[b, i] == sequence_id[b, j] (:186-191; NULL = no mask); fp32 scores and
