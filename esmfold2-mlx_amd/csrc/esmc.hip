@@ -142,116 +142,104 @@ __global__ __launch_bounds__(NTR) void esmc_ln_kernel(EsmcLnArgs p) {
 }
 
 // ---- QK-LayerNorm + RoPE, head-major outputs ---------------------------------------------------
-// Thread -> chunks of 8 rotation pairs: chunk u < D/16 of q, else of k (u' = u mod D/16);
-// pairs (e, e + 32) of head u' / 4 at e = 8 (u' % 4) .. + 7, so a chunk is two 16-byte
-// loads and two 16-byte stores. The LayerNorm statistics of q and k are reduced together.
-// Every load is issued first (v's chunks, then the q/k chunks through a range-checked
-// descriptor of the row, then their LayerNorm weights), and v leaves as soon as it has
-// arrived, so the row's memory latencies overlap instead of following one another.
-__global__ __launch_bounds__(NTR) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
-  __shared__ float red[2][4];
-  constexpr int HD = 64, HALF = 32, MAXC = 2, MAXV = 2;  // 2 D / 16 and D / 8 <= MAXC * NTR for D <= 4096
-  const int row = blockIdx.x, D = p.H * HD, nq = D / 16;
+// One thread per chunk of 8 rotation pairs: chunk u < D/16 of q, else of k (u' = u mod D/16);
+// pairs (e, e + 32) of head u' / 4 at e = 8 (u' % 4) .. + 7, so a chunk is two 16-byte loads
+// and two 16-byte stores; thread t also moves v's 8 halfs at 8 t. The workgroup has
+// roundup(D/8, 64) threads (the D/8 chunks of q and k; 320 at D = 2560, at most 512), so no
+// wave carries a second chunk. Every load is issued first (v, the q/k chunk through a
+// range-checked descriptor of the row, its LayerNorm weights) and v leaves as soon as it has
+// arrived. The LayerNorm statistics of q and k are reduced together.
+constexpr int kRopeMaxThreads = 512;
+DEV float2v wg_sum2_n(float a, float b, float (*red)[kRopeMaxThreads / 64]) {
+  a = row16_sum(a);
+  b = row16_sum(b);
+  a += __shfl_xor(a, 16);
+  b += __shfl_xor(b, 16);
+  a += __shfl_xor(a, 32);
+  b += __shfl_xor(b, 32);
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();  // red is reused by consecutive calls
+  if ((threadIdx.x & 63) == 0) {
+    red[0][w] = a;
+    red[1][w] = b;
+  }
+  __syncthreads();
+  float sa = red[0][0], sb = red[1][0];
+  for (int k = 1; k < nw; k++) {
+    sa += red[0][k];
+    sb += red[1][k];
+  }
+  return float2v{sa, sb};
+}
+
+__global__ __launch_bounds__(kRopeMaxThreads) void esmc_qk_rope_kernel(EsmcRopeArgs p) {
+  __shared__ float red[2][kRopeMaxThreads / 64];
+  constexpr int HD = 64, HALF = 32;
+  const int row = blockIdx.x, D = p.H * HD, nq = D / 16, t = threadIdx.x;
   const int b = row / p.L, l = row - b * p.L;
   const half_t* src = p.qkv + (size_t)row * 3 * D;
   const rsrc_t rs = make_rsrc_n(src, (uint32_t)(3 * D) * 2u);
-  half8 vv[MAXV], x1[MAXC], x2[MAXC];
-  f32x4 wl[MAXC][4];
+  const int ev = 8 * t;
+  const half8 vv = bload16(rs, ev < D ? (uint32_t)(2 * D + ev) * 2u : kOOB);
+  const bool ok = t < 2 * nq;
+  const int which = t >= nq, uu = t - which * nq, hh = uu >> 2, i0 = 8 * (uu & 3);
+  const uint32_t off = (uint32_t)(which * D + hh * HD + i0) * 2u;
+  const half8 x1 = bload16(rs, ok ? off : kOOB), x2 = bload16(rs, ok ? off + 2u * HALF : kOOB);
+  const float* w = ok ? (which ? p.k_ln : p.q_ln) + hh * HD + i0 : p.q_ln;
+  const f32x4 w0 = *reinterpret_cast<const f32x4*>(w), w1 = *reinterpret_cast<const f32x4*>(w + 4);
+  const f32x4 w2 = *reinterpret_cast<const f32x4*>(w + HALF), w3 = *reinterpret_cast<const f32x4*>(w + HALF + 4);
+  if (ev < D) st16(p.v + (((size_t)b * p.H + ev / HD) * p.L + l) * HD + ev % HD, vv);  // v: head-major
+
+  float a[8], c[8], sq = 0.f, sk = 0.f;
 #pragma unroll
-  for (int k = 0; k < MAXV; k++) {
-    const int e = 8 * (threadIdx.x + NTR * k);
-    vv[k] = bload16(rs, e < D ? (uint32_t)(2 * D + e) * 2u : kOOB);
-  }
+  for (int e = 0; e < 8; e++) a[e] = c[e] = 0.f;
+  if (ok) {
+    float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < MAXC; j++) {
-    const int u = threadIdx.x + NTR * j;
-    const bool ok = u < 2 * nq;
-    const int which = u >= nq, uu = u - which * nq;
-    const uint32_t off = (uint32_t)(which * D + (uu >> 2) * HD + 8 * (uu & 3)) * 2u;
-    x1[j] = bload16(rs, ok ? off : kOOB);
-    x2[j] = bload16(rs, ok ? off + 2u * HALF : kOOB);
-  }
-#pragma unroll
-  for (int j = 0; j < MAXC; j++) {
-    const int u = threadIdx.x + NTR * j;
-    const int which = u >= nq, uu = u - which * nq;
-    const float* w = u < 2 * nq ? (which ? p.k_ln : p.q_ln) + (uu >> 2) * HD + 8 * (uu & 3) : p.q_ln;
-    wl[j][0] = *reinterpret_cast<const f32x4*>(w);
-    wl[j][1] = *reinterpret_cast<const f32x4*>(w + 4);
-    wl[j][2] = *reinterpret_cast<const f32x4*>(w + HALF);
-    wl[j][3] = *reinterpret_cast<const f32x4*>(w + HALF + 4);
-  }
-  // v: head-major, 8 halfs per thread
-#pragma unroll
-  for (int k = 0; k < MAXV; k++) {
-    const int e = 8 * (threadIdx.x + NTR * k);
-    if (e < D) {
-      const int hh = e / HD, d = e % HD;
-      st16(p.v + (((size_t)b * p.H + hh) * p.L + l) * HD + d, vv[k]);
+    for (int e = 0; e < 8; e++) {
+      a[e] = (float)x1[e];
+      c[e] = (float)x2[e];
+      s += a[e] + c[e];
     }
+    sq += which ? 0.f : s;
+    sk += which ? s : 0.f;
   }
-  float a[MAXC][8], c[MAXC][8], sq = 0.f, sk = 0.f;
-#pragma unroll
-  for (int j = 0; j < MAXC; j++) {
-    const int u = threadIdx.x + NTR * j;
-#pragma unroll
-    for (int e = 0; e < 8; e++) a[j][e] = c[j][e] = 0.f;
-    if (u < 2 * nq) {
-      const int which = u >= nq;
-      float t = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        a[j][e] = (float)x1[j][e];
-        c[j][e] = (float)x2[j][e];
-        t += a[j][e] + c[j][e];
-      }
-      sq += which ? 0.f : t;
-      sk += which ? t : 0.f;
-    }
-  }
-  float2v sum = wg_sum2(sq, sk, red);
+  float2v sum = wg_sum2_n(sq, sk, red);
   const float mq = sum[0] / D, mk = sum[1] / D;
   sq = sk = 0.f;
+  if (ok) {
+    const float mean = which ? mk : mq;
+    float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < MAXC; j++) {
-    const int u = threadIdx.x + NTR * j;
-    if (u < 2 * nq) {
-      const float mean = u >= nq ? mk : mq;
-      float t = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        a[j][e] -= mean;
-        c[j][e] -= mean;
-        t += a[j][e] * a[j][e] + c[j][e] * c[j][e];
-      }
-      sq += u >= nq ? 0.f : t;
-      sk += u >= nq ? t : 0.f;
+    for (int e = 0; e < 8; e++) {
+      a[e] -= mean;
+      c[e] -= mean;
+      s += a[e] * a[e] + c[e] * c[e];
     }
+    sq += which ? 0.f : s;
+    sk += which ? s : 0.f;
   }
-  sum = wg_sum2(sq, sk, red);
+  sum = wg_sum2_n(sq, sk, red);
   const float rq = rsqrtf(sum[0] / D + p.eps), rk = rsqrtf(sum[1] / D + p.eps);
+  if (ok) {
+    const float rstd = which ? rk : rq;
+    const float wl[16] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3],
+                          w2[0], w2[1], w2[2], w2[3], w3[0], w3[1], w3[2], w3[3]};
+    half8 o1, o2;
 #pragma unroll
-  for (int j = 0; j < MAXC; j++) {
-    const int u = threadIdx.x + NTR * j;
-    if (u < 2 * nq) {
-      const int which = u >= nq, uu = u - which * nq, hh = uu >> 2, i0 = 8 * (uu & 3);
-      const float rstd = which ? rk : rq;
-      half8 o1, o2;
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const int i = i0 + e;
-        // rotation angle of pair i: l * base^(-2i/hd)
-        const float ang = (float)l * exp2f(-(float)(2 * i) / HD * p.log2_base);
-        float sn, cs;
-        sincosf(ang, &sn, &cs);
-        const float x1v = a[j][e] * rstd * wl[j][e >> 2][e & 3], x2v = c[j][e] * rstd * wl[j][2 + (e >> 2)][e & 3];
-        o1[e] = (half_t)(x1v * cs - x2v * sn);
-        o2[e] = (half_t)(x2v * cs + x1v * sn);
-      }
-      half_t* o = (which ? p.k : p.q) + (((size_t)b * p.H + hh) * p.L + l) * HD + i0;
-      st16(o, o1);
-      st16(o + HALF, o2);
+    for (int e = 0; e < 8; e++) {
+      const int i = i0 + e;
+      // rotation angle of pair i: l * base^(-2i/hd)
+      const float ang = (float)l * exp2f(-(float)(2 * i) / HD * p.log2_base);
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      const float x1v = a[e] * rstd * wl[e], x2v = c[e] * rstd * wl[8 + e];
+      o1[e] = (half_t)(x1v * cs - x2v * sn);
+      o2[e] = (half_t)(x2v * cs + x1v * sn);
     }
+    half_t* o = (which ? p.k : p.q) + (((size_t)b * p.H + hh) * p.L + l) * HD + i0;
+    st16(o, o1);
+    st16(o + HALF, o2);
   }
 }
 
@@ -500,7 +488,10 @@ hipError_t launch_esmc_ln(const EsmcLnArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s) {
-  ESM_LAUNCH(esmc_qk_rope_kernel, dim3(a.B * a.L), dim3(NTR), 0, s, a);
+  const int D = a.H * 64, chunks = 2 * (D / 16) > D / 8 ? 2 * (D / 16) : D / 8;  // q/k chunks, v chunks
+  const int nthr = (chunks + 63) / 64 * 64;
+  if (nthr > kRopeMaxThreads) return hipErrorInvalidValue;  // D <= 4096 is checked by the caller
+  ESM_LAUNCH(esmc_qk_rope_kernel, dim3(a.B * a.L), dim3(nthr), 0, s, a);
   return hipGetLastError();
 }
 
