@@ -464,16 +464,17 @@ namespace {
 constexpr int SBM = 64;   // cells per tile
 }  // namespace
 
-// The epilogue of wide_value with the mask (HM) and the residual (RS) fixed per launch.
+// The epilogue of wide_value with the mask (HM) and the residual (RS) fixed per launch; mv is
+// the cell's mask value (staged in LDS with the tile).
 template <int EPI, bool HM, bool RS>
-DEV float wide_value_u(const WideArgs& p, float d1, float d2, size_t cell, bool in, float zv) {
+DEV float wide_value_u(float d1, float d2, float mv, bool in, float zv) {
   float v;
   if constexpr (EPI == kWideGateCM) {
     v = d1 * sigmoidf_fast(d2);
-    if constexpr (HM) v *= in ? (float)p.mask[cell] : 0.f;
+    if constexpr (HM) v *= in ? mv : 0.f;
   } else if constexpr (EPI == kWideResGate) {
     v = d1 * sigmoid_from_t(d2 * kNegLog2e);
-    if constexpr (HM) v *= in ? (float)p.mask[cell] : 0.f;
+    if constexpr (HM) v *= in ? mv : 0.f;
     if constexpr (RS) v += zv;
   } else if constexpr (EPI == kWideRelu) {
     v = fmaxf(d1, 0.f);
@@ -487,8 +488,10 @@ DEV float wide_value_u(const WideArgs& p, float d1, float d2, size_t cell, bool 
 
 // FRAG (the channel-major epilogue only): tiles of 8 x 8 cells, operand rows line .. line+7
 // by k pos0 .. pos0+7 (tile cell c = 8 dr + dc), and the a, b planes written in FragLayout,
-// one whole 128-byte segment per channel and tile.
-template <int EPI, bool DUAL, bool A2SEP, int KW, bool FRAG = false>
+// one whole 128-byte segment per channel and tile. HM (the gating epilogues only): the
+// epilogue multiplies by the mask, whose values for a tile's cells are loaded with its A rows
+// and staged in LDS; without it the kernel holds no mask code at all.
+template <int EPI, bool DUAL, bool A2SEP, int KW, bool FRAG = false, bool HM = false>
 __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   constexpr int K = 16 * KW;
   constexpr int KS = K / 32;                    // k-steps of the 16x16x32 MFMA
@@ -510,6 +513,7 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
   static_assert(!(CM && ZR), "no residual with channel-major planes");
   static_assert(!FRAG || CM, "the fragment layout is for the channel-major planes");
   __shared__ __align__(16) char smem_c[SMEM_BYTES];
+  __shared__ __align__(16) float m_s[HM ? SBM : 4];  // the tile's mask values
   half_t* a_s = reinterpret_cast<half_t*>(smem_c);
   half_t* os = reinterpret_cast<half_t*>(smem_c + A_HALFS * 2);
 
@@ -560,9 +564,11 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
       return ps < L;
     }
   };
+  static_assert(!HM || EPI == kWideGateCM || EPI == kWideResGate, "the mask is a gating epilogue's");
   struct Regs {
     half8 a[NA][CH_A];
     half4 z[ZR ? NOB : 1][ZR ? 4 : 1];          // z[cell 16 cb + l16][outputs ob + 4 q4 .. +3]
+    uint16_t mk;                                // threads 0 .. SBM-1: the mask of tile cell tid
   };
   // One tile's loads: the A rows (row-contiguous 16-byte pieces), and the residual pieces
   // this lane adds, 8 bytes each. The descriptors start at the tile's first cell (line, pos0):
@@ -582,6 +588,12 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
       const uint32_t off = ok ? (uint32_t)((cell_of(bi, ln, ps) - c0) * K + 8 * j) * 2u : kOOB;
       r.a[0][u] = bload16(rA1, off);
       if constexpr (A2SEP) r.a[1][u] = bload16(rA2, off);
+    }
+    if constexpr (HM) {  // one mask value per tile cell, loaded with the A rows
+      const rsrc_t rM = make_rsrc(p.mask + c0);
+      int ln, ps;
+      const bool ok = live && tid < SBM && tcell(line, pos0, tid, ln, ps);
+      r.mk = bload2(rM, ok ? (uint32_t)(cell_of(bi, ln, ps) - c0) * 2u : kOOB);
     }
     if constexpr (ZR) {
       const bool want = EPI == kWideResid || p.residual;
@@ -610,6 +622,8 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
         const int id = tid + WNT * u, row = id / (K / 8), j = id - row * (K / 8);
         st16(a_s + (pa * SBM + row) * AS + 8 * j, ra.a[pa][u]);
       }
+    if constexpr (HM)
+      if (tid < SBM) m_s[tid] = h2f(ra.mk);
     __syncthreads();  // the A tiles are in LDS; the previous tile's staging reads are done
     f32x4 acc[2][4];
 #pragma unroll
@@ -630,8 +644,21 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
           acc[f][cb] = CM ? mfma16(af, wf[f][ks], acc[f][cb]) : mfma16(wf[f][ks], af, acc[f][cb]);
         }
       }
-    auto finish = [&](auto hm, auto rs) {
-      constexpr bool HM = decltype(hm)::value, RS = decltype(rs)::value;
+    // the MFMA block is scheduled on its own (LDS reads kept ahead of their products), apart
+    // from the epilogue's transcendental arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+    auto finish = [&](auto rs) {
+      constexpr bool RS = decltype(rs)::value;
+      f32x4 mv[4];  // the mask of this lane's cells (all four LDS reads issued before the first use)
+#pragma unroll
+      for (int cb = 0; cb < 4; cb++) {
+        if constexpr (!HM)
+          mv[cb] = f32x4{1.f, 1.f, 1.f, 1.f};
+        else if constexpr (CM)
+          mv[cb] = *reinterpret_cast<const f32x4*>(m_s + 16 * cb + 4 * q4);
+        else
+          mv[cb] = f32x4{m_s[16 * cb + l16], m_s[16 * cb + l16], m_s[16 * cb + l16], m_s[16 * cb + l16]};
+      }
 #pragma unroll
       for (int b = 0; b < NOB; b++)
 #pragma unroll
@@ -649,7 +676,7 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
             }
             const float d1 = acc[DUAL ? 0 : b][cb][e], d2 = DUAL ? acc[1][cb][e] : 0.f;
             const float zv = ZR ? (float)ra.z[ZR ? b : 0][ZR ? cb : 0][e] : 0.f;  // zeros past the ends
-            float v = wide_value_u<EPI, HM, RS>(p, d1, d2, HM ? cell_of(bi, ln, ps) : 0, in, zv);
+            float v = wide_value_u<EPI, HM, RS>(d1, d2, mv[cb][e], in, zv);
             // fp32 first, then fp16, at every position: left to itself the compiler fuses the
             // last multiply with the conversion (one rounding) at some accumulator positions
             // only, so a cell's bits would depend on where the tiling puts it
@@ -662,15 +689,10 @@ __global__ __launch_bounds__(WNT, 1) void wide_gemm_ws_kernel(WideArgs p) {
             *reinterpret_cast<half4*>(os + (16 * cb + l16) * OS + ob0 + 16 * b + 4 * q4) = hv;
         }
     };
-    const bool hm = (EPI == kWideGateCM && p.mask) || (EPI == kWideResGate && p.mask && p.out_mask);
-    const bool rs = EPI == kWideResid || (EPI == kWideResGate && p.residual);
-    using T_ = std::true_type;
-    using F_ = std::false_type;
-    if (hm) {
-      if (rs) finish(T_{}, T_{}); else finish(T_{}, F_{});
-    } else {
-      if (rs) finish(F_{}, T_{}); else finish(F_{}, F_{});
-    }
+    if (EPI == kWideResid || (EPI == kWideResGate && p.residual))
+      finish(std::true_type{});
+    else
+      finish(std::false_type{});
     __syncthreads();  // the staged tile is complete; every wave is done with the A tiles
     if constexpr (CM && FRAG) {
       // chunk q of a channel's staged row: operand row line + q, k pos0 .. pos0+7, lane
@@ -830,14 +852,21 @@ static hipError_t launch_wide_gemm_ws(const WideArgs& a, int epi, int cus, hipSt
   switch (epi) {                                                                                             \
     case kWideGateCM:                                                                                        \
       if (!dual || sep) return hipErrorInvalidValue;                                                         \
-      if (a.frag)                                                                                            \
-        ESM_LAUNCH((wide_gemm_ws_kernel<kWideGateCM, true, false, KW, true>), grid, block, 0, s, a); \
+      if (a.frag && a.mask)                                                                                  \
+        ESM_LAUNCH((wide_gemm_ws_kernel<kWideGateCM, true, false, KW, true, true>), grid, block, 0, s, a);   \
+      else if (a.frag)                                                                                       \
+        ESM_LAUNCH((wide_gemm_ws_kernel<kWideGateCM, true, false, KW, true>), grid, block, 0, s, a);         \
+      else if (a.mask)                                                                                       \
+        ESM_LAUNCH((wide_gemm_ws_kernel<kWideGateCM, true, false, KW, false, true>), grid, block, 0, s, a);  \
       else                                                                                                   \
-        ESM_LAUNCH((wide_gemm_ws_kernel<kWideGateCM, true, false, KW>), grid, block, 0, s, a);       \
+        ESM_LAUNCH((wide_gemm_ws_kernel<kWideGateCM, true, false, KW>), grid, block, 0, s, a);               \
       break;                                                                                                 \
     case kWideResGate:                                                                                       \
       if (!dual || !sep) return hipErrorInvalidValue;                                                        \
-      ESM_LAUNCH((wide_gemm_ws_kernel<kWideResGate, true, true, KW>), grid, block, 0, s, a);         \
+      if (a.mask && a.out_mask)                                                                              \
+        ESM_LAUNCH((wide_gemm_ws_kernel<kWideResGate, true, true, KW, false, true>), grid, block, 0, s, a);  \
+      else                                                                                                   \
+        ESM_LAUNCH((wide_gemm_ws_kernel<kWideResGate, true, true, KW>), grid, block, 0, s, a);               \
       break;                                                                                                 \
     case kWideRelu:                                                                                          \
       if (dual) return hipErrorInvalidValue;                                                                 \
