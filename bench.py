@@ -18,11 +18,12 @@ Also reported on the same JSON line:
   kernels       the same figures for every kernel of the step, and for the
                 contraction its fraction of its own roof, min(MFMA peak, AI x HBM
                 peak) with AI = L/3 FLOP/B by compulsory traffic;
-  q8            the 8-bit ESMC-style linears [238,2560]x[2560->10240] and
-                [238,10240]x[10240->2560] (time, TFLOP/s, GB/s) on the weight layout
-                Q8Linear keeps (codes and scales packed once per layer), the time
-                with the codes in MLX's [N, K] layout beside it, and each launch's
-                own duration;
+  q8            the 8-bit ESMC-style linears [238,2560]x[2560->10240],
+                [238,10240]x[10240->2560] and [238,2560]x[2560->7680] (time, TFLOP/s,
+                GB/s, the output tile's weight rows the plan picked) on the weight
+                layout Q8Linear keeps (codes and scales packed once per layer), the
+                time with the codes in MLX's [N, K] layout beside it, and each
+                launch's own duration;
   transition    the pair transition kernel (LN -> 128->512 -> ReLU -> 512->128 + z)
                 at L=238 (time, TFLOP/s, fraction of MFMA peak);
   block_stack   the pair-trunk block stack at L=238: 8 blocks of (T_out, T_in,
@@ -422,7 +423,7 @@ def main():
     q8_samples = {}
     if not args.no_q8:
         qres = {}
-        for (Kd, Nd) in ((2560, 10240), (10240, 2560)):
+        for (Kd, Nd) in ((2560, 10240), (10240, 2560), (2560, 7680)):
             xq, qq, sq, bq = W.q8_inputs(L, Kd, Nd, seed=Kd)
             xt, qt, st, bt = (t.to(dev) for t in (xq, qq, sq, bq))
             y = torch.empty(L, Nd, dtype=torch.float16, device=dev)
@@ -453,7 +454,8 @@ def main():
             by = Nd * Kd + 2 * 2 * Nd * (Kd // 64) + 2 * L * Kd + 2 * L * Nd
             qres[name] = {"us": t * 1e6, "tflops": fl / t / 1e12, "mfma_frac": fl / t / MFMA_F16_PEAK,
                           "gbs": by / t / 1e9, "hbm_frac": by / t / HBM_PEAK, "split_k": ws is not None,
-                          "layout": "packed codes and scales (Q8Linear's default)", "us_nk_codes": t_nk * 1e6}
+                          "layout": "packed codes and scales (Q8Linear's default)", "us_nk_codes": t_nk * 1e6,
+                          "tile_rows": int(pkg.capi.lib().q8_tile_rows(L, Kd, Nd))}
             # each launch's own duration (runtime-stamped events, a pass of its own): with split-K the
             # GEMM and the reduction of its partials separately, the reduction being the launch a
             # consumer that sums the partials itself (the ESMC block's LayerNorm) does not make

@@ -59,6 +59,8 @@ SIGNATURES = {
     "q8_linear_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "q8_linear_workspace_bytes": (_sz, [_int, _int, _int]),
     "q8_linear_partials_bytes": (_sz, [_int, _int, _int]),
+    "q8_tile_rows": (_int, [_int, _int, _int]),
+    "q8_set_tile_rows": (_int, [_int]),
     "q8_linear_partials": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _int, _int, _int, _int, _vp]),
     "q8_packed_scales_bytes": (_sz, [_int, _int]),
     "q8_pack_scales": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp]),

@@ -3,6 +3,7 @@
 // memory; every launch goes on the caller's stream.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -60,20 +61,32 @@ int cu_count() {
 // (32 x 2 x L^2 bytes: 1.07 GB at 4096) and kernel (c) reads 16 channel rows (0.5 GB).
 constexpr int kMaxL = 4096;
 
-// q8 GEMM launch plan. A tile is kQ8TileM x kQ8TileN outputs; when the tiles alone
-// cannot fill the GPU, K is split over up to kQ8MaxSplits workgroups per tile (each
-// of the 4 waves keeps at least one 64-wide group) and the partials go through the
-// caller's workspace: [splits, M, N] fp32, summed by a second kernel.
+// q8 GEMM launch plan. A tile is kQ8TileM x 32 nb outputs, nb = 4 (128 weight rows) or 5
+// (160). When the tiles alone cannot fill the GPU, K is split over up to kQ8MaxSplits
+// workgroups per tile (each of the 4 waves keeps at least one 64-wide group) and the
+// partials go through the caller's workspace: [splits, M, N] fp32, summed by a second
+// kernel. The width is the one with the lower estimate of rounds x steps per workgroup x
+// the time of a step (a 128-row step takes ~0.9 of a 160-row one, ~0.7 us at K = 2560 on
+// 256 CUs), plus, when K is split, writing and reading back the partials (~4 TB/s).
+// Measured at M = 238, 128 against 160 rows: N = 7680 unsplit 20.8 against 22.5 us (also
+// inside the ESMC block's graph); N = 2560 split at K = 2560 10.9 against 11.2 in the graph
+// (16.6 against 19.1 alone with the reduction kernel), at K = 5120 16.0 against 15.3 in the
+// graph (21.2 against 22.2 alone), at K = 10240 31.8 against 29.4 alone; N = 10240 takes 160
+// rows (256 tiles, one round; 320 at 128 rows). A SwiGLU-pair weight always takes the wide tile, whose 80 + 80
+// rows the pair order is laid out for.
 constexpr int kQ8MaxSplits = 16;
 constexpr int kQ8MaxK = 1 << 20;  // keeps every per-row byte offset far below 2^31
+constexpr double kQ8StepUs = 0.7, kQ8NarrowStep = 0.9, kQ8PartialBytesPerUs = 4.0e6;
+std::atomic<int> g_q8_tile_rows{0};  // q8_set_tile_rows: 0 lets the plan choose
 struct Q8Plan {
-  int mtiles, ntiles, splits;
+  int mtiles, ntiles, splits, nb;
   size_t bytes;
 };
-Q8Plan q8_plan(int M, int K, int N) {
+Q8Plan q8_plan_nb(int M, int K, int N, int nb) {
   Q8Plan p;
+  p.nb = nb;
   p.mtiles = (M + esm::kQ8TileM - 1) / esm::kQ8TileM;
-  p.ntiles = (N + esm::kQ8TileN - 1) / esm::kQ8TileN;
+  p.ntiles = (N + 32 * nb - 1) / (32 * nb);
   const long long tiles = (long long)p.mtiles * p.ntiles;
   const int groups = K / 64;
   long long sp = cu_count() / tiles;
@@ -82,6 +95,20 @@ Q8Plan q8_plan(int M, int K, int N) {
   p.splits = sp < 1 ? 1 : (int)sp;
   p.bytes = (size_t)p.splits * M * N * sizeof(float);
   return p;
+}
+double q8_plan_cost(const Q8Plan& p, int M, int K, int N) {
+  const long long cus = cu_count(), wgs = (long long)p.mtiles * p.ntiles * p.splits;
+  const long long rounds = (wgs + cus - 1) / cus, steps = ((K / 64 + 1) / 2 + p.splits - 1) / p.splits;
+  double c = (double)rounds * (double)steps * kQ8StepUs * (p.nb == esm::kQ8TileNbWide ? 1.0 : kQ8NarrowStep);
+  if (p.splits > 1) c += p.splits * (double)M * N * 8.0 / kQ8PartialBytesPerUs;
+  return c;
+}
+Q8Plan q8_plan(int M, int K, int N, bool swiglu = false) {
+  const int forced = g_q8_tile_rows.load() / 32;
+  if (swiglu) return q8_plan_nb(M, K, N, esm::kQ8TileNbWide);
+  if (forced) return q8_plan_nb(M, K, N, forced);
+  const Q8Plan narrow = q8_plan_nb(M, K, N, esm::kQ8TileNbNarrow), wide = q8_plan_nb(M, K, N, esm::kQ8TileNbWide);
+  return q8_plan_cost(narrow, M, K, N) <= q8_plan_cost(wide, M, K, N) ? narrow : wide;
 }
 
 #ifndef ESM_SOURCE_HASH
@@ -502,7 +529,7 @@ int q8_linear_ws(const esm_half* x, const uint8_t* q, const esm_half* s, const e
   }
   if (sb && !aligned16(sb)) return fail(ESM_ERR_ALIGN, "q8_linear: packed scales must be 16-byte aligned");
   esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits,
-                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb, nullptr};
+                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb, nullptr, 0, pl.nb};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear launch");
 }
 
@@ -524,7 +551,7 @@ int q8_linear_noalloc(const esm_half* x, const uint8_t* q, const esm_half* s, co
     const hipError_t e = esm::q8_scratch_address(&part);
     if (e != hipSuccess) return hip_status(e, "q8_linear_noalloc: scratch address");
   }
-  esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits, part, sb, nullptr};
+  esm::Q8Args a{H(x), q, H(s), H(b), H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits, part, sb, nullptr, 0, pl.nb};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_noalloc launch");
 }
 
@@ -547,7 +574,7 @@ int q8_linear_partials(const esm_half* x, const uint8_t* q, const esm_half* s, c
     return fail(ESM_ERR_SHAPE, "q8_linear_partials: %zu bytes for the partials, %zu needed", parts_bytes, pl.bytes);
   if (sb && !aligned16(sb)) return fail(ESM_ERR_ALIGN, "q8_linear_partials: packed scales must be 16-byte aligned");
   *splits = pl.splits;
-  esm::Q8Args a{H(x), q, H(s), H(b), nullptr, M, K, N, pl.mtiles, pl.ntiles, pl.splits, parts, sb, nullptr};
+  esm::Q8Args a{H(x), q, H(s), H(b), nullptr, M, K, N, pl.mtiles, pl.ntiles, pl.splits, parts, sb, nullptr, 0, pl.nb};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_partials launch");
 }
 
@@ -571,7 +598,7 @@ int q8_linear_packed_ws(const esm_half* x, const uint8_t* qp, const uint32_t* sb
       return fail(ESM_ERR_ALIGN, "q8_linear_packed_ws: workspace must be 256-byte aligned");
   }
   esm::Q8Args a{H(x), nullptr, nullptr, nullptr, H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits,
-                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb, qp};
+                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb, qp, 0, pl.nb};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_packed_ws launch");
 }
 
@@ -586,7 +613,7 @@ int q8_linear_swiglu_packed_ws(const esm_half* x, const uint8_t* qp, const uint3
   if (N % (2 * esm::kQ8SwigluHalf) != 0)
     return fail(ESM_ERR_SHAPE, "q8_linear_swiglu_packed_ws: N=%d must be a multiple of %d (SwiGLU pair tiles)", N,
                 2 * esm::kQ8SwigluHalf);
-  Q8Plan pl = q8_plan(M, K, N);
+  Q8Plan pl = q8_plan(M, K, N, true);
   if ((long long)pl.mtiles * pl.ntiles * pl.splits > 0x7fffffffLL)
     return fail(ESM_ERR_SHAPE, "q8_linear_swiglu_packed_ws: M=%d N=%d too large", M, N);
   if (!workspace) {
@@ -599,7 +626,7 @@ int q8_linear_swiglu_packed_ws(const esm_half* x, const uint8_t* qp, const uint3
       return fail(ESM_ERR_ALIGN, "q8_linear_swiglu_packed_ws: workspace must be 256-byte aligned");
   }
   esm::Q8Args a{H(x), nullptr, nullptr, nullptr, H(y), M, K, N, pl.mtiles, pl.ntiles, pl.splits,
-                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb, qp, 1};
+                pl.splits > 1 ? static_cast<float*>(workspace) : nullptr, sb, qp, 1, pl.nb};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_swiglu_packed_ws launch");
 }
 
@@ -620,7 +647,7 @@ int q8_linear_packed_partials(const esm_half* x, const uint8_t* qp, const uint32
     return fail(ESM_ERR_SHAPE, "q8_linear_packed_partials: %zu bytes for the partials, %zu needed", parts_bytes,
                 pl.bytes);
   *splits = pl.splits;
-  esm::Q8Args a{H(x), nullptr, nullptr, nullptr, nullptr, M, K, N, pl.mtiles, pl.ntiles, pl.splits, parts, sb, qp};
+  esm::Q8Args a{H(x), nullptr, nullptr, nullptr, nullptr, M, K, N, pl.mtiles, pl.ntiles, pl.splits, parts, sb, qp, 0, pl.nb};
   return hip_status(esm::launch_q8_linear(a, (hipStream_t)stream), "q8_linear_packed_partials launch");
 }
 
@@ -825,7 +852,7 @@ int abs_diff_quantile(const float* x, const float* y, size_t n, float q, float* 
 
 size_t q8_packed_scales_bytes(int N, int K) {
   if (N <= 0 || K <= 0 || K % 64 != 0) return 0;
-  return (size_t)((N + esm::kQ8TileN - 1) / esm::kQ8TileN) * (K / 64) * esm::kQ8TileN * sizeof(uint32_t);
+  return esm::q8_packed_scales_words(N, K) * sizeof(uint32_t);
 }
 
 int q8_pack_scales(const esm_half* s, const esm_half* b, uint32_t* sb, int N, int K, int group, void* stream) {
@@ -859,8 +886,23 @@ int q8_pack_codes(const uint8_t* q, uint8_t* qp, int N, int K, int group, void* 
 
 size_t q8_linear_workspace_bytes(int M, int K, int N) {
   if (M <= 0 || K <= 0 || N <= 0 || K % 64 != 0 || N % 64 != 0 || K > kQ8MaxK) return 0;
-  const Q8Plan pl = q8_plan(M, K, N);
-  return pl.splits > 1 ? pl.bytes : 0;
+  // enough for the plain and the SwiGLU plan of the shape (their tile widths may differ)
+  const Q8Plan pl = q8_plan(M, K, N), ps = q8_plan(M, K, N, true);
+  const size_t a = pl.splits > 1 ? pl.bytes : 0, b = ps.splits > 1 ? ps.bytes : 0;
+  return a > b ? a : b;
+}
+
+int q8_set_tile_rows(int rows) {
+  if (rows != 0 && rows != 32 * esm::kQ8TileNbNarrow && rows != 32 * esm::kQ8TileNbWide)
+    return fail(ESM_ERR_SHAPE, "q8_set_tile_rows: rows=%d (0, %d or %d)", rows, 32 * esm::kQ8TileNbNarrow,
+                32 * esm::kQ8TileNbWide);
+  g_q8_tile_rows.store(rows);
+  return ok();
+}
+
+int q8_tile_rows(int M, int K, int N) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  return 32 * q8_plan(M, K, N).nb;
 }
 
 int q8_quantize(const float* w, uint8_t* q, esm_half* s, esm_half* b, int N, int K, int group, void* stream) {

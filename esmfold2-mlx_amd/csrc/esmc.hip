@@ -464,6 +464,8 @@ static hipError_t launch_esmc_ln_nj(const EsmcLnArgs& a, hipStream_t s) {
   const int ns = a.yp ? a.splits : 0;
   if (ns == 4)
     ESM_LAUNCH((esmc_ln_kernel<NJ, 4>), dim3(a.M), dim3(NTR), 0, s, a);
+  else if (ns == 3)
+    ESM_LAUNCH((esmc_ln_kernel<NJ, 3>), dim3(a.M), dim3(NTR), 0, s, a);
   else if (ns == 2)
     ESM_LAUNCH((esmc_ln_kernel<NJ, 2>), dim3(a.M), dim3(NTR), 0, s, a);
   else if (ns == 1)

@@ -72,18 +72,21 @@ struct Q8Args {
   const half_t* b;      // [N, K/64]
   half_t* y;            // [M, N]
   int M, K, N;
-  int mtiles, ntiles;   // tiles of kQ8TileM x kQ8TileN outputs
+  int mtiles, ntiles;   // tiles of kQ8TileM x (32 nb) outputs
   int splits;           // K ranges per tile
   float* part;          // [splits, M, N] fp32 partials, or nullptr: y written directly (splits 1)
-  const uint32_t* sb;   // packed scales [ntiles, K/64, kQ8TileN] (b << 16 | s), or nullptr
+  const uint32_t* sb;   // packed scales [N/32, K/64, 32] (b << 16 | s), or nullptr
   const uint8_t* qp;    // codes packed by q8_pack_codes (needs sb), or nullptr: q is read
   int swiglu;           // weight rows in SwiGLU pairs (each 160-row tile: 80 gate rows, then the
                         // matching 80 up rows): y [M, N/2] = silu(gate) * up instead of [M, N]
+  int nb;               // 32-row weight blocks per tile: kQ8TileNbNarrow or kQ8TileNbWide
 };
 
-// q8 GEMM tile: kQ8TileM rows of x by kQ8TileN weight rows, kQ8Waves waves per workgroup.
+// q8 GEMM tile: kQ8TileM rows of x by 32 nb weight rows (nb = 4 or 5, chosen per call by the
+// launch plan), kQ8Waves waves per workgroup. The packed layouts do not depend on nb.
 constexpr int kQ8TileM = 64;
-constexpr int kQ8TileN = 160;
+constexpr int kQ8TileNbNarrow = 4;
+constexpr int kQ8TileNbWide = 5;
 constexpr int kQ8Waves = 4;
 // Bytes of the device scratch q8_linear_noalloc keeps its split-K partials in.
 constexpr size_t kQ8ScratchBytes = (size_t)16 << 20;
@@ -214,11 +217,13 @@ hipError_t launch_esmc_qk_rope(const EsmcRopeArgs& a, hipStream_t s);
 hipError_t launch_esmc_attention(const EsmcAttnArgs& a, hipStream_t s);
 hipError_t launch_esmc_swiglu(const half_t* x12, half_t* y, size_t M, int F, hipStream_t s);
 hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st);
-// Bytes of q8_pack_codes' layout: per 160-row tile and step of two groups, 4 waves x 5
-// row blocks x 64 lanes x 16 bytes.
+// Bytes of q8_pack_codes' layout: per 32-row block and step of two groups, 4 waves x 64
+// lanes x 16 bytes.
 constexpr size_t q8_packed_codes_size(int N, int K) {
-  return (size_t)((N + kQ8TileN - 1) / kQ8TileN) * (size_t)((K / 64 + 1) / 2) * (size_t)(kQ8Waves * 5 * 1024);
+  return (size_t)((N + 31) / 32) * (size_t)((K / 64 + 1) / 2) * (size_t)(kQ8Waves * 1024);
 }
+// Words of q8_pack_scales' layout: per 32-row block and group, 32 words b << 16 | s.
+constexpr size_t q8_packed_scales_words(int N, int K) { return (size_t)((N + 31) / 32) * (size_t)(K / 64) * 32; }
 hipError_t launch_q8_pack_codes(const uint8_t* q, uint8_t* qp, int N, int K, hipStream_t st);
 hipError_t launch_ln_rows(const void* x, const float* x2, bool in_f32, const float* w, const float* b, float eps,
                           half_t* out, size_t rows, int C, hipStream_t s);

@@ -7,14 +7,16 @@
 // subtracts 1024 (exact: q), v_pk_fma_f16 gives RN(s*q + b) with one rounding. The
 // same bits as the dequantise entry point.
 //
-// Tiling: a workgroup owns a 64 (m) x 160 (n) tile of y = 2 x 5 blocks of the
-// 32x32x16 MFMA, and a range of K, walked in steps of two 64-wide groups (128 k).
-// Each step's codes (160 rows x 128 B), x (64 rows x 256 B) and packed scales are
-// loaded with row-contiguous 16-byte loads (8 or 16 lanes per row, one step ahead in
-// registers) and stored to one of two LDS stages; one barrier per step. Wave w then
-// takes MFMA step kk = w of both groups: every wave accumulates the whole tile (10
+// Tiling: a workgroup owns a 64 (m) x 32 NB (n) tile of y = 2 x NB blocks of the
+// 32x32x16 MFMA (NB = 5, 160 rows, or 4, 128 rows: the launch plan picks the width that
+// fills the GPU in the fewest rounds), and a range of K, walked in steps of two 64-wide
+// groups (128 k). Each step's codes (32 NB rows x 128 B), x (64 rows x 256 B) and packed
+// scales are loaded with row-contiguous 16-byte loads (8 or 16 lanes per row, one step
+// ahead in registers) and stored to one of two LDS stages; one barrier per step. Wave w
+// then takes MFMA step kk = w of both groups: every wave accumulates the whole tile (2 NB
 // independent chains) over its quarter of each step's k, so every dequantised weight
-// feeds 64 rows of x and no two waves dequantise the same weight. (Loading the MFMA
+// feeds 64 rows of x and no two waves dequantise the same weight. Each output's sum runs
+// over the same k in the same order at either width: the same bits. (Loading the MFMA
 // fragments straight from global memory instead puts 32 rows in every load
 // instruction, i.e. 32 to 64 cache lines for 1 KB, and measured 1.8x slower.)
 // Weight codes dominate the traffic (1 byte per MAC row); M-tiles of the same n-tile
@@ -36,11 +38,9 @@ namespace esm {
 
 namespace {
 constexpr int QG = 64;           // quantisation group: k per step
-constexpr int NBQ = 5;           // 32-row n blocks per tile
 constexpr int MBQ = 2;           // 32-row m blocks per tile
 constexpr int NWQ = 4;           // waves per workgroup
-constexpr int NBLK = MBQ * NBQ;  // accumulator blocks per tile
-static_assert(kQ8TileN == 32 * NBQ && kQ8TileM == 32 * MBQ && kQ8Waves == NWQ, "tile geometry");
+static_assert(kQ8TileM == 32 * MBQ && kQ8Waves == NWQ, "tile geometry");
 }  // namespace
 
 DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
@@ -69,44 +69,66 @@ DEV half2v splat2(uint32_t bits) {
   return half2v{v, v};
 }
 
-// LDS stage of one step (two groups, 128 k) of a tile. Codes: 160 rows of 128 B at a
+// LDS stage of one step (two groups, 128 k) of a tile. Codes: TN rows of 128 B at a
 // 136-byte stride (rows start on 32 distinct even banks: the 8-byte fragment reads of
 // 32 rows are conflict-free); x: 64 rows of 256 B at a 272-byte stride (16 rows per
 // 16-byte read pass on distinct banks); scale/bias pairs packed (b << 16 | s) per group.
 constexpr int QSTR = 136, XSTR = 272;
-constexpr int QSTAGE = kQ8TileN * QSTR, XSTAGE = kQ8TileM * XSTR, SBSTAGE = 2 * kQ8TileN * 4;
-constexpr int STAGE = QSTAGE + XSTAGE + SBSTAGE;
 constexpr int NT = NWQ * 64;
-constexpr int QCH = kQ8TileN * 8 / NT;   // 16-byte code chunks per thread per step (5)
+constexpr int XSTAGE = kQ8TileM * XSTR;
 constexpr int XCH = kQ8TileM * 16 / NT;  // 16-byte x chunks per thread per step (4)
-constexpr int RED_BYTES = NWQ * NBLK * 4 * 64 * 16;
-static_assert(kQ8TileN * 8 % NT == 0 && kQ8TileM * 16 % NT == 0 && kQ8TileN <= NT, "loader split");
-static_assert(2 * STAGE <= RED_BYTES, "stages fit in the reduction area");
+template <int NB>
+struct Q8Geo {
+  static constexpr int TN = 32 * NB;                       // weight rows per tile
+  static constexpr int NBLK = MBQ * NB;                    // accumulator blocks per tile
+  static constexpr int QSTAGE = TN * QSTR, SBSTAGE = 2 * TN * 4;
+  static constexpr int STAGE = QSTAGE + XSTAGE + SBSTAGE;
+  static constexpr int QCH = TN * 8 / NT;                  // 16-byte code chunks per thread per step
+  static constexpr int RED_BYTES = NWQ * NBLK * 4 * 64 * 16;
+  static constexpr int SBT = 16 * NB;                      // threads that load a step's packed scale words
+  static_assert(TN * 8 % NT == 0 && kQ8TileM * 16 % NT == 0 && TN <= NT && SBT <= NT, "loader split");
+  static_assert(2 * STAGE <= RED_BYTES, "stages fit in the reduction area");
+};
 
 // One step's global loads of one thread (registers, issued a step ahead of their LDS store).
+template <int NB>
 struct Q8Load {
-  u32x4 q[QCH];
+  u32x4 q[Q8Geo<NB>::QCH];
   u32x4 x[XCH];
-  u32x4 sbv;                  // packed scales: 4 (b << 16 | s) words of the step's 320
+  u32x4 sbv;                  // packed scales: 4 (b << 16 | s) words of the step's 64 NB
   uint32_t s0, s1, b0, b1;    // unpacked: one row's two groups
 };
-constexpr int SBT = 2 * kQ8TileN / 4;  // threads that load a step's packed scale words
 
-// PACKED: scales and biases come pre-packed per tile ([n-tile][group][160] words of
-// b << 16 | s, from q8_pack_scales): a step's 320 words are 1280 contiguous bytes, one
-// 16-byte load for 80 threads. Unpacked, every thread of the first 160 reads its row's
-// fp16 pairs from the [N, K/64] arrays: 160 scattered rows per step, several times the
+// Packed scales [N/32][K/64][32] words: a step's two groups of one 32-row block are 64
+// consecutive words. Thread i < 16 NB loads 4 of them: block i / 16, group i % 16 / 8,
+// rows 4 (i % 8) .. + 3. Its byte offset from the tile's first block (kOOB for the second
+// group of a step that has one), and where the words go in the [2][TN] LDS stage.
+DEV uint32_t sb_offset(int i, int g, int ngroups, bool two) {
+  const int nb = i >> 4, pc = i & 15;
+  return (pc < 8 || two) ? (((uint32_t)nb * ngroups + g) * 32u + 4u * pc) * 4u : kOOB;
+}
+template <int NB>
+DEV int sb_slot(int i) {
+  return ((i & 15) >> 3) * Q8Geo<NB>::TN + 32 * (i >> 4) + 4 * (i & 7);
+}
+
+// PACKED: scales and biases come pre-packed per 32-row block ([N/32][group][32] words of
+// b << 16 | s, from q8_pack_scales): a step's words of one block are 256 contiguous bytes,
+// one 16-byte load for 16 threads. Unpacked, every thread of the first TN reads its row's
+// fp16 pairs from the [N, K/64] arrays: TN scattered rows per step, several times the
 // L1 requests of the codes and x together.
 //
 // PCODES: the codes come packed by q8_pack_codes, each MFMA A-fragment's 8 codes of both groups
-// of a step next to each other for its lane: a wave loads its 5 fragments of a step as 5 fully
+// of a step next to each other for its lane: a wave loads its NB fragments of a step as NB fully
 // coalesced 1 KB loads straight into registers (two steps ahead), and only x and the scales
-// pass through LDS (43 instead of 73 KB of LDS traffic per step). Same MFMAs in the same
-// order: the same bits as the [N, K] codes.
-template <bool PACKED, bool PCODES>
+// pass through LDS (43 instead of 73 KB of LDS traffic per step at NB = 5). Same MFMAs in the
+// same order: the same bits as the [N, K] codes.
+template <bool PACKED, bool PCODES, int NB>
 __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
   static_assert(PACKED || !PCODES, "packed codes are read with packed scales");
-  __shared__ __align__(16) char smem[RED_BYTES];  // two step stages, then every wave's partial tile
+  using G = Q8Geo<NB>;
+  constexpr int TN = G::TN, NBLK = G::NBLK, QSTAGE = G::QSTAGE, STAGE = G::STAGE, QCH = G::QCH, SBT = G::SBT;
+  __shared__ __align__(16) char smem[G::RED_BYTES];  // two step stages, then every wave's partial tile
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -120,7 +142,7 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
   t /= p.mtiles;
   const int nt = t % p.ntiles;
   const int sp = t / p.ntiles;
-  const int m0 = mt * kQ8TileM, n0 = nt * kQ8TileN;
+  const int m0 = mt * kQ8TileM, n0 = nt * TN;
   const int K = p.K, M = p.M, N = p.N, ngroups = K / QG;
   // This split's steps [st0, st1) of two groups each (whole steps, so a split starts where a
   // packed step does), i.e. groups [sg0, sg1).
@@ -138,11 +160,13 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
   const rsrc_t rb = PACKED ? make_rsrc_n(p.x, 0u)
                            : make_rsrc_n(p.b + (size_t)n0 * ngroups, (uint32_t)(N - n0) * (uint32_t)ngroups * 2u);
   const rsrc_t rx = make_rsrc_n(p.x + (size_t)m0 * K, (uint32_t)(M - m0) * (uint32_t)K * 2u);
-  const rsrc_t rsb = make_rsrc_n(PACKED ? (const void*)(p.sb + (size_t)nt * ngroups * kQ8TileN) : (const void*)p.x,
-                                 PACKED ? (uint32_t)ngroups * kQ8TileN * 4u : 0u);
+  // the tile's blocks of the packed layouts (blocks past N are out of range: zeros)
+  const int blk0 = n0 / 32, nblk = (N + 31) / 32 - blk0 < NB ? (N + 31) / 32 - blk0 : NB;
+  const rsrc_t rsb = make_rsrc_n(PACKED ? (const void*)(p.sb + (size_t)blk0 * ngroups * 32) : (const void*)p.x,
+                                 PACKED ? (uint32_t)nblk * (uint32_t)ngroups * 128u : 0u);
 
   // Coalesced loads: 8 lanes per 128-byte code row piece, 16 lanes per 256-byte x row piece.
-  auto gload = [&](Q8Load& ld, int step) {
+  auto gload = [&](Q8Load<NB>& ld, int step) {
     const int g = sg0 + 2 * step;
     const bool two = g + 1 < sg1;
 #pragma unroll
@@ -157,17 +181,16 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
       ld.x[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
     }
     if (PACKED) {
-      ld.sbv = __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(tid < SBT ? ((uint32_t)g * kQ8TileN + 4u * tid) * 4u : kOOB),
-                                                     0, 0);
+      ld.sbv = __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(tid < SBT ? sb_offset(tid, g, ngroups, two) : kOOB), 0, 0);
     } else {
-      const uint32_t so = tid < kQ8TileN ? ((uint32_t)tid * ngroups + g) * 2u : kOOB;
+      const uint32_t so = tid < TN ? ((uint32_t)tid * ngroups + g) * 2u : kOOB;
       ld.s0 = bload2(rs, so);
       ld.s1 = bload2(rs, so + 2u);
       ld.b0 = bload2(rb, so);
       ld.b1 = bload2(rb, so + 2u);
     }
   };
-  auto sstore = [&](const Q8Load& ld, int buf) {
+  auto sstore = [&](const Q8Load<NB>& ld, int buf) {
     char* st = smem + buf * STAGE;
 #pragma unroll
     for (int i = 0; i < QCH; i++) {
@@ -183,18 +206,18 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     }
     uint32_t* sb = reinterpret_cast<uint32_t*>(st + QSTAGE + XSTAGE);
     if (PACKED) {
-      if (tid < SBT) *reinterpret_cast<u32x4*>(sb + 4 * tid) = ld.sbv;
-    } else if (tid < kQ8TileN) {
+      if (tid < SBT) *reinterpret_cast<u32x4*>(sb + sb_slot<NB>(tid)) = ld.sbv;
+    } else if (tid < TN) {
       sb[tid] = (ld.b0 << 16) | (ld.s0 & 0xffffu);
-      sb[kQ8TileN + tid] = (ld.b1 << 16) | (ld.s1 & 0xffffu);
+      sb[TN + tid] = (ld.b1 << 16) | (ld.s1 & 0xffffu);
     }
   };
 
-  f32x16 acc[MBQ][NBQ];
+  f32x16 acc[MBQ][NB];
 #pragma unroll
   for (int mb = 0; mb < MBQ; mb++)
 #pragma unroll
-    for (int nb = 0; nb < NBQ; nb++)
+    for (int nb = 0; nb < NB; nb++)
 #pragma unroll
       for (int i = 0; i < 16; i++) acc[mb][nb][i] = 0.f;
 
@@ -205,11 +228,11 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     const uint32_t* sb = reinterpret_cast<const uint32_t*>(st + QSTAGE + XSTAGE);
 #pragma unroll
     for (int g = 0; g < 2; g++) {
-      half8 a[NBQ];
+      half8 a[NB];
 #pragma unroll
-      for (int nb = 0; nb < NBQ; nb++) {
+      for (int nb = 0; nb < NB; nb++) {
         const int row = 32 * nb + r;
-        const uint32_t w = sb[g * kQ8TileN + row];
+        const uint32_t w = sb[g * TN + row];
         const u32x2 c = *reinterpret_cast<const u32x2*>(st + row * QSTR + 64 * g + 16 * wave + 8 * kg);
         a[nb] = dequant8(c[0], c[1], splat2(w & 0xffffu), splat2(w >> 16));
       }
@@ -218,7 +241,7 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
       for (int mb = 0; mb < MBQ; mb++)
         xf[mb] = *reinterpret_cast<const half8*>(st + QSTAGE + (32 * mb + r) * XSTR + 128 * g + 32 * wave + 16 * kg);
 #pragma unroll
-      for (int nb = 0; nb < NBQ; nb++)
+      for (int nb = 0; nb < NB; nb++)
 #pragma unroll
         for (int mb = 0; mb < MBQ; mb++) acc[mb][nb] = mfma32(a[nb], xf[mb], acc[mb][nb]);
     }
@@ -228,7 +251,7 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     // Pipeline: step s+2's loads in flight while step s computes from LDS and step s+1's
     // registers wait to be stored; one barrier per step. Unrolled by two (register sets
     // A and B), a single loop exit, the leftover step after it.
-    Q8Load la, lb;
+    Q8Load<NB> la, lb;
     if (nsteps > 0) {
       gload(la, 0);
       gload(lb, 1);
@@ -248,16 +271,19 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     }
     if (st < nsteps) compute(0);
   } else {
-    // Codes of step s (this wave's 5 fragments) in register set A or B from two steps before;
-    // x and the scales staged as above, in a stage without the codes area.
-    constexpr int XS = XSTAGE + SBSTAGE;
-    constexpr size_t kStepBytes = (size_t)NWQ * NBQ * 1024;  // one step of one n-tile
-    const rsrc_t rqp = make_rsrc_n(p.qp + ((size_t)nt * S + st0) * kStepBytes, (uint32_t)(nsteps * kStepBytes));
-    auto gcodes = [&](u32x4 (&cq)[NBQ], int step) {
+    // Codes of step s (this wave's NB fragments) in register set A or B from two steps before;
+    // x and the scales staged as above, in a stage without the codes area. Packed codes
+    // [N/32][S][4 waves][64 lanes][16 B]: fragment nb of a step is 1 KB at block blk0 + nb.
+    constexpr int XS = XSTAGE + G::SBSTAGE;
+    constexpr uint32_t kWaveStep = NWQ * 1024;  // one step of one 32-row block
+    const rsrc_t rqp = make_rsrc_n(p.qp + (size_t)blk0 * S * kWaveStep, (uint32_t)nblk * (uint32_t)S * kWaveStep);
+    auto gcodes = [&](u32x4 (&cq)[NB], int step) {
 #pragma unroll
-      for (int nb = 0; nb < NBQ; nb++)
+      for (int nb = 0; nb < NB; nb++)
         cq[nb] = __builtin_amdgcn_raw_buffer_load_b128(
-            rqp, (int)(step < nsteps ? (uint32_t)(((step * NWQ + wave) * NBQ + nb) * 1024 + lane * 16) : kOOB), 0, 0);
+            rqp,
+            (int)(step < nsteps ? ((uint32_t)nb * S + st0 + step) * kWaveStep + (uint32_t)(wave * 1024 + lane * 16) : kOOB),
+            0, 0);
     };
     auto xload = [&](u32x4 (&xv)[XCH], u32x4& sbv, int step) {
       const int g = sg0 + 2 * step;
@@ -268,8 +294,7 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
         const uint32_t off = (j < 8 || two) ? ((uint32_t)row * K + g * QG) * 2u + 16u * j : kOOB;
         xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
       }
-      sbv = __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(tid < SBT ? ((uint32_t)g * kQ8TileN + 4u * tid) * 4u : kOOB),
-                                                  0, 0);
+      sbv = __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(tid < SBT ? sb_offset(tid, g, ngroups, two) : kOOB), 0, 0);
     };
     auto xstore = [&](const u32x4 (&xv)[XCH], const u32x4& sbv, int buf) {
       char* st = smem + buf * XS;
@@ -278,17 +303,17 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
         const int c = tid + NT * i, row = c >> 4, j = c & 15;
         *reinterpret_cast<u32x4*>(st + row * XSTR + 16 * j) = xv[i];
       }
-      if (tid < SBT) *reinterpret_cast<u32x4*>(reinterpret_cast<uint32_t*>(st + XSTAGE) + 4 * tid) = sbv;
+      if (tid < SBT) *reinterpret_cast<u32x4*>(reinterpret_cast<uint32_t*>(st + XSTAGE) + sb_slot<NB>(tid)) = sbv;
     };
-    auto compute_pc = [&](int buf, const u32x4 (&cq)[NBQ]) {
+    auto compute_pc = [&](int buf, const u32x4 (&cq)[NB]) {
       const char* st = smem + buf * XS;
       const uint32_t* sb = reinterpret_cast<const uint32_t*>(st + XSTAGE);
 #pragma unroll
       for (int g = 0; g < 2; g++) {
-        half8 a[NBQ];
+        half8 a[NB];
 #pragma unroll
-        for (int nb = 0; nb < NBQ; nb++) {
-          const uint32_t w = sb[g * kQ8TileN + 32 * nb + r];
+        for (int nb = 0; nb < NB; nb++) {
+          const uint32_t w = sb[g * TN + 32 * nb + r];
           a[nb] = dequant8(cq[nb][2 * g], cq[nb][2 * g + 1], splat2(w & 0xffffu), splat2(w >> 16));
         }
         half8 xf[MBQ];
@@ -296,12 +321,12 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
         for (int mb = 0; mb < MBQ; mb++)
           xf[mb] = *reinterpret_cast<const half8*>(st + (32 * mb + r) * XSTR + 128 * g + 32 * wave + 16 * kg);
 #pragma unroll
-        for (int nb = 0; nb < NBQ; nb++)
+        for (int nb = 0; nb < NB; nb++)
 #pragma unroll
           for (int mb = 0; mb < MBQ; mb++) acc[mb][nb] = mfma32(a[nb], xf[mb], acc[mb][nb]);
       }
     };
-    u32x4 xa[XCH], xb[XCH], sa, sbb, ca[NBQ], cb[NBQ];
+    u32x4 xa[XCH], xb[XCH], sa, sbb, ca[NB], cb[NB];
     if (nsteps > 0) {
       xload(xa, sa, 0);
       gcodes(ca, 0);
@@ -332,10 +357,10 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
 #pragma unroll
   for (int mb = 0; mb < MBQ; mb++)
 #pragma unroll
-    for (int nb = 0; nb < NBQ; nb++)
+    for (int nb = 0; nb < NB; nb++)
 #pragma unroll
       for (int r4 = 0; r4 < 4; r4++)
-        red[wave][mb * NBQ + nb][r4][lane] =
+        red[wave][mb * NB + nb][r4][lane] =
             f32x4{acc[mb][nb][4 * r4], acc[mb][nb][4 * r4 + 1], acc[mb][nb][4 * r4 + 2], acc[mb][nb][4 * r4 + 3]};
   __syncthreads();
 
@@ -346,17 +371,17 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
     for (int w = 1; w < NWQ; w++) v += red[w][blk][r4][lane];
     return v;
   };
-  if (p.part == nullptr && p.swiglu) {
-    // SwiGLU pairs: a lane's 4 gate rows n .. n+3 (n = 32 nb + 8 r4 + 4 h < 80) have their up
-    // rows at n + 80 = 32 (nb + 2) + 8 (r4 + 2) + 4 h: the same lane's sums in block nb + 2 or
-    // nb + 3. Both round to fp16 as y would, then silu(gate) * up in fp32 as esmc_swiglu does.
+  if constexpr (NB == kQ8TileNbWide) if (p.part == nullptr && p.swiglu) {
+    // SwiGLU pairs (160-row tiles only): a lane's 4 gate rows n .. n+3 (n = 32 nb + 8 r4 + 4 h
+    // < 80) have their up rows at n + 80 = 32 (nb + 2) + 8 (r4 + 2) + 4 h: the same lane's sums
+    // in block nb + 2 or nb + 3. Both round to fp16 as y would, then silu(gate) * up in fp32 as esmc_swiglu does.
     constexpr int HALF = kQ8SwigluHalf, NG = MBQ * HALF / 8;  // gate groups of 8 rows per tile
     const int F = N / 2;
     for (int gi = wave; gi < NG; gi += NWQ) {
       const int mb = gi / (HALF / 8), g8 = gi - mb * (HALF / 8);  // gate rows 8 g8 .. 8 g8 + 7
       const int nb = g8 >> 2, r4 = g8 & 3;
       const int ru = r4 + 2, nbu = nb + 2 + (ru >> 2);
-      const f32x4 g = tile_sum(mb * NBQ + nb, r4), u = tile_sum(mb * NBQ + nbu, ru & 3);
+      const f32x4 g = tile_sum(mb * NB + nb, r4), u = tile_sum(mb * NB + nbu, ru & 3);
       const int m = m0 + 32 * mb + r, f = nt * HALF + 8 * g8 + 4 * kg;
       half4 o;
 #pragma unroll
@@ -370,7 +395,7 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
   }
   if (p.part == nullptr) {  // one K range per tile: fp16 y directly
     for (int blk = wave; blk < NBLK; blk += NWQ) {
-      const int mb = blk / NBQ, nb = blk - mb * NBQ;
+      const int mb = blk / NB, nb = blk - mb * NB;
       const int m = m0 + 32 * mb + r;
 #pragma unroll
       for (int r4 = 0; r4 < 4; r4++) {
@@ -387,7 +412,7 @@ __global__ __launch_bounds__(NWQ * 64, 1) void q8_linear_kernel(Q8Args p) {
   // or the consumer (esmc_ln_kernel) sums the splits.
   float* part = p.part + (size_t)sp * M * N;
   for (int blk = wave; blk < NBLK; blk += NWQ) {
-    const int mb = blk / NBQ, nb = blk - mb * NBQ;
+    const int mb = blk / NB, nb = blk - mb * NB;
     const int m = m0 + 32 * mb + r;
 #pragma unroll
     for (int r4 = 0; r4 < 4; r4++) {
@@ -451,35 +476,35 @@ __global__ __launch_bounds__(256) void q8_dequant_kernel(const uint8_t* __restri
   }
 }
 
-// sb[(t * ngroups + g) * 160 + j] = b[n, g] << 16 | s[n, g] for n = 160 t + j (0 past N).
+// sb[(j * ngroups + g) * 32 + r] = b[n, g] << 16 | s[n, g] for n = 32 j + r (0 past N): per
+// 32-row block, so a tile of any whole number of blocks reads its words at one base.
 __global__ __launch_bounds__(256) void q8_pack_kernel(const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
                                                       uint32_t* __restrict__ sb, int N, int ngroups, size_t total) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int j = (int)(i % kQ8TileN);
-    const size_t rest = i / kQ8TileN;
+    const int r = (int)(i % 32);
+    const size_t rest = i / 32;
     const int g = (int)(rest % ngroups);
-    const int n = (int)(rest / ngroups) * kQ8TileN + j;
+    const int n = (int)(rest / ngroups) * 32 + r;
     sb[i] = n < N ? ((uint32_t)b[(size_t)n * ngroups + g] << 16) | s[(size_t)n * ngroups + g] : 0u;
   }
 }
 
-// Codes in the order q8_linear_kernel<true, true> reads them: chunk ((t S + s) 4 + w) 5 + nb,
-// lane l, 16 bytes = the codes of row 160 t + 32 nb + l % 32 at k = 128 s + 16 w + 8 (l / 32)
-// + 0..7 (group 2s), then the same k + 64 (group 2s+1); zeros past N and past K. One thread
-// per 16-byte chunk.
+// Codes in the order q8_linear_kernel<true, true, NB> reads them: chunk ((j S + s) 4 + w),
+// lane l, 16 bytes = the codes of row 32 j + l % 32 at k = 128 s + 16 w + 8 (l / 32) + 0..7
+// (group 2s), then the same k + 64 (group 2s+1); zeros past N and past K. A 32-row block's
+// steps are consecutive, so a tile of any whole number of blocks reads its fragments at one
+// base. One thread per 16-byte chunk.
 __global__ __launch_bounds__(256) void q8_pack_codes_kernel(const uint8_t* __restrict__ q, uint8_t* __restrict__ qp,
                                                             int N, int K, size_t nchunks) {
   const int S = (K / QG + 1) / 2;
   for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < nchunks; c += (size_t)gridDim.x * blockDim.x) {
     const int lane = (int)(c % 64);
     size_t rest = c / 64;
-    const int nb = (int)(rest % NBQ);
-    rest /= NBQ;
     const int w = (int)(rest % NWQ);
     rest /= NWQ;
     const int s = (int)(rest % S);
-    const int t = (int)(rest / S);
-    const int n = t * kQ8TileN + 32 * nb + (lane & 31);
+    const int j = (int)(rest / S);
+    const int n = 32 * j + (lane & 31);
     const int k0 = 128 * s + 16 * w + 8 * (lane >> 5);
     u32x2 lo = {0u, 0u}, hi = {0u, 0u};
     if (n < N) {
@@ -499,8 +524,8 @@ hipError_t launch_q8_pack_codes(const uint8_t* q, uint8_t* qp, int N, int K, hip
 }
 
 hipError_t launch_q8_pack(const half_t* s, const half_t* b, uint32_t* sb, int N, int K, hipStream_t st) {
-  const int ngroups = K / QG, ntiles = (N + kQ8TileN - 1) / kQ8TileN;
-  const size_t total = (size_t)ntiles * ngroups * kQ8TileN;
+  const int ngroups = K / QG;
+  const size_t total = q8_packed_scales_words(N, K);
   const size_t blocks = (total + 255) / 256;
   ESM_LAUNCH(q8_pack_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st,
                      reinterpret_cast<const uint16_t*>(s), reinterpret_cast<const uint16_t*>(b), sb, N, ngroups, total);
@@ -539,12 +564,20 @@ hipError_t q8_scratch_address(float** ptr) {
 hipError_t launch_q8_linear(const Q8Args& a, hipStream_t s) {
   const int grid = a.mtiles * a.ntiles * a.splits;
   if (a.qp && !a.sb) return hipErrorInvalidValue;
-  if (a.qp)
-    ESM_LAUNCH((q8_linear_kernel<true, true>), dim3(grid), dim3(NWQ * 64), 0, s, a);
-  else if (a.sb)
-    ESM_LAUNCH((q8_linear_kernel<true, false>), dim3(grid), dim3(NWQ * 64), 0, s, a);
-  else
-    ESM_LAUNCH((q8_linear_kernel<false, false>), dim3(grid), dim3(NWQ * 64), 0, s, a);
+  if (a.nb != kQ8TileNbWide && (a.nb != kQ8TileNbNarrow || a.swiglu)) return hipErrorInvalidValue;
+#define Q8_LAUNCH(NB)                                                                  \
+  if (a.qp)                                                                            \
+    ESM_LAUNCH((q8_linear_kernel<true, true, NB>), dim3(grid), dim3(NWQ * 64), 0, s, a);  \
+  else if (a.sb)                                                                       \
+    ESM_LAUNCH((q8_linear_kernel<true, false, NB>), dim3(grid), dim3(NWQ * 64), 0, s, a); \
+  else                                                                                 \
+    ESM_LAUNCH((q8_linear_kernel<false, false, NB>), dim3(grid), dim3(NWQ * 64), 0, s, a);
+  if (a.nb == kQ8TileNbWide) {
+    Q8_LAUNCH(kQ8TileNbWide)
+  } else {
+    Q8_LAUNCH(kQ8TileNbNarrow)
+  }
+#undef Q8_LAUNCH
   if (a.part && a.y && a.swiglu) {  // partials of SwiGLU pair rows: summed and gated here
     const size_t n4 = (size_t)a.M * (a.N / 2) / 4, blocks = (n4 + 255) / 256;
     ESM_LAUNCH(q8_reduce_swiglu_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, s, a.part, a.y,

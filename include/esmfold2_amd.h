@@ -274,9 +274,9 @@ int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_
  * q8_linear with the two optional speed-ups a long-lived caller (a layer holding its
  * weights) can afford:
  *   sb: the scales and biases pre-packed by q8_pack_scales (once per weight matrix);
- *       NULL reads them from s and b (slower: 160 scattered rows per 128-wide step).
- *   workspace: for shapes whose output tiles (64 x 160) are too few to fill the GPU
- *       (e.g. M = 238, N = 2560), K is split over several workgroups whose fp32
+ *       NULL reads them from s and b (slower: 128-160 scattered rows per 128-wide step).
+ *   workspace: for shapes whose output tiles (64 x 128 or 64 x 160, q8_tile_rows) are too
+ *       few to fill the GPU (e.g. M = 238, N = 2560), K is split over several workgroups whose fp32
  *       partials go through the workspace and are summed in split order by a second
  *       kernel on the same stream (deterministic). q8_linear_workspace_bytes(M, K, N)
  *       bytes, 256-byte aligned, no initialisation needed; NULL runs unsplit. Calls
@@ -287,8 +287,22 @@ int q8_linear(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_
 int q8_linear_ws(const esm_half* x, const uint8_t* q, const esm_half* s, const esm_half* b, const uint32_t* sb,
                  esm_half* y, int M, int K, int N, int group, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes q8_linear_ws uses for this shape on the current device (0: none). */
+/* Workspace bytes q8_linear_ws (or q8_linear_swiglu_packed_ws) uses for this shape on the
+ * current device (0: none). */
 size_t q8_linear_workspace_bytes(int M, int K, int N);
+
+/*
+ * The weight rows per output tile the launch plan picks for this shape on the current
+ * device: 128 when those tiles fit in one round of the GPU's CUs, else 160 when those do,
+ * else the width with fewer rounds per unit of work (160 always for the SwiGLU-pair call).
+ * Either width gives the same bits when K is not split (it only changes which workgroup
+ * computes an output); with a K split the split count, and so the fp32 summation order,
+ * can differ. q8_set_tile_rows(128 or 160) fixes the width for every later plan of this
+ * process (0 restores the choice; tests and tuning). No reference counterpart: the
+ * reference's quantized_matmul (mlx_esmc.py:78-81) tiles inside MLX.
+ */
+int q8_tile_rows(int M, int K, int N);
+int q8_set_tile_rows(int rows);
 
 /*
  * The GEMM of q8_linear_ws without its last step: the fp32 partial sums of y go to
@@ -307,19 +321,19 @@ int q8_linear_partials(const esm_half* x, const uint8_t* q, const esm_half* s, c
                        float* parts, size_t parts_bytes, int* splits, int M, int K, int N, int group, void* stream);
 
 /*
- * Packs s and b [N, K/group] fp16 into sb [ceil(N/160), K/group, 160] uint32 words
- * (b << 16 | s; rows past N are 0), the layout q8_linear_ws reads a step of in one
- * coalesced load. A layout cache of the reference's fp16 scales/biases
- * (mlx_esmc.py:53-75), built once per weight matrix. group = 64.
+ * Packs s and b [N, K/group] fp16 into sb [ceil(N/32), K/group, 32] uint32 words
+ * (b << 16 | s; rows past N are 0): per 32-row block, so a tile of either width reads a
+ * step's words as 256-byte contiguous pieces. A layout cache of the reference's fp16
+ * scales/biases (mlx_esmc.py:53-75), built once per weight matrix. group = 64.
  */
 size_t q8_packed_scales_bytes(int N, int K);
 int q8_pack_scales(const esm_half* s, const esm_half* b, uint32_t* sb, int N, int K, int group, void* stream);
 
 /*
  * Packs the codes q [N, K] (MLX's layout, one byte per weight) into qp in the order the
- * GEMM's matrix-core fragments take them: per 160-row tile and step of two groups (128 k),
- * 4 x 5 chunks of 1 KB, one 16-byte piece per lane; rows past N and groups past K/group
- * are 0. q8_packed_codes_bytes(N, K) bytes (about N K; 0 for an unsupported shape), qp
+ * GEMM's matrix-core fragments take them: per 32-row block and step of two groups (128 k),
+ * 4 chunks of 1 KB (one per wave), one 16-byte piece per lane; rows past N and groups past
+ * K/group are 0. Independent of the tile width. q8_packed_codes_bytes(N, K) bytes (about N K; 0 for an unsupported shape), qp
  * 16-byte aligned, q 8-byte aligned. A layout cache of the reference's 8-bit weights
  * (mlx_esmc.py:53-75), built once per weight matrix like q8_pack_scales. group = 64.
  */

@@ -111,7 +111,8 @@ def test_rejects_null_and_bad_shapes(lib):
         assert "eps" in _err(lib)
     assert lib.q8_pack_scales(None, None, None, 64, 128, 64, None) == -1
     assert lib.q8_pack_scales(None, None, None, 64, 100, 64, None) == -2
-    assert lib.q8_packed_scales_bytes(64, 128) == 1 * 2 * 160 * 4 and lib.q8_packed_scales_bytes(161, 64) == 2 * 160 * 4
+    # per 32-row block and 64-group, 32 words
+    assert lib.q8_packed_scales_bytes(64, 128) == 2 * 2 * 32 * 4 and lib.q8_packed_scales_bytes(161, 64) == 6 * 32 * 4
     # split-K workspace: too small, then misaligned (both rejected before any launch)
     need = lib.q8_linear_workspace_bytes(5, 1024, 64)
     assert need > 0 and lib.q8_linear_workspace_bytes(238, 2560, 10240) == 0
@@ -135,9 +136,9 @@ def test_rejects_null_and_bad_shapes(lib):
 
 
 def test_packed_codes_entry_points_validate(lib):
-    # sizes: per 160-row tile and step of two 64-groups, 4 x 5 chunks of 1 KB
-    assert lib.q8_packed_codes_bytes(160, 128) == 20480
-    assert lib.q8_packed_codes_bytes(161, 192) == 2 * 2 * 20480  # 3 groups -> 2 steps, 2 tiles
+    # sizes: per 32-row block and step of two 64-groups, 4 chunks of 1 KB
+    assert lib.q8_packed_codes_bytes(160, 128) == 5 * 4096
+    assert lib.q8_packed_codes_bytes(161, 192) == 6 * 2 * 4096  # 3 groups -> 2 steps, 6 blocks
     assert lib.q8_packed_codes_bytes(64, 100) == 0 and lib.q8_packed_codes_bytes(0, 64) == 0
     assert lib.q8_pack_codes(None, None, 64, 128, 64, None) == -1
     assert lib.q8_pack_codes(None, None, 64, 128, 32, None) == -4
@@ -235,3 +236,27 @@ def test_python_wrappers_refuse_cpu_tensors(pkg):
     p = tmu.draw_weights(torch.Generator().manual_seed(0), 128, 128, True)
     with pytest.raises(Exception):
         pkg.trimul.TriMul.from_weights(p, device="cpu")(torch.zeros(1, 4, 4, 128))
+
+
+def test_q8_tile_rows_plan_and_override(lib):
+    # without a GPU the plan assumes 256 CUs: 4 m-tiles x 60 (128 rows) fit one round; 4 x 80 take
+    # two where 4 x 64 (160 rows) take one; tiny shapes take 128
+    assert lib.q8_tile_rows(238, 2560, 7680) == 128 and lib.q8_tile_rows(238, 2560, 10240) == 160
+    assert lib.q8_tile_rows(7, 64, 64) == 128
+    # split K: 7 steps per workgroup in 3 splits (128 rows) against 5 in 4 (160 rows) and one
+    # split's partials less to write and read: 128; at K = 5120 (14 against 10) and K = 10240
+    # (27 against 20) the steps outweigh the partials: 160
+    assert lib.q8_tile_rows(238, 2560, 2560) == 128
+    assert lib.q8_tile_rows(238, 5120, 2560) == 160 and lib.q8_tile_rows(238, 10240, 2560) == 160
+    # 16 m-tiles: 960 narrow (4 rounds) against 768 wide (3 rounds): 3 x 10 <= 4 x 9 -> 160
+    assert lib.q8_tile_rows(1024, 2560, 7680) == 160
+    assert lib.q8_tile_rows(0, 64, 64) == 0
+    assert lib.q8_set_tile_rows(96) == -2 and "q8_set_tile_rows" in _err(lib)
+    try:
+        assert lib.q8_set_tile_rows(160) == 0 and lib.q8_tile_rows(238, 2560, 7680) == 160
+        assert lib.q8_set_tile_rows(128) == 0 and lib.q8_tile_rows(238, 2560, 10240) == 128
+    finally:
+        assert lib.q8_set_tile_rows(0) == 0
+    assert lib.q8_tile_rows(238, 2560, 10240) == 160
+    # the workspace covers the SwiGLU plan too (160-row tiles: more K splits at small M)
+    assert lib.q8_linear_workspace_bytes(50, 2560, 10240) == 4 * 50 * 10240 * 4

@@ -5,6 +5,8 @@ Bars: dequantised weights bit-exact against RN_fp16(s*q + b); the GEMM within
 1e-3 * max|ref|).
 """
 
+import contextlib
+
 import numpy as np
 import pytest
 import torch
@@ -17,6 +19,17 @@ DEV = "cuda"
 
 def _t(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+@contextlib.contextmanager
+def _tile_rows(pkg, rows):
+    # every q8 plan in the block uses output tiles of `rows` weight rows (0: the plan's choice)
+    lib = pkg.capi.lib()
+    pkg.capi.check(lib.q8_set_tile_rows(rows))
+    try:
+        yield
+    finally:
+        pkg.capi.check(lib.q8_set_tile_rows(0))
 
 
 @pytest.mark.parametrize("N,K", [(64, 64), (128, 192), (256, 2560)])
@@ -89,8 +102,8 @@ def test_q8_linear_rejects_bad_shapes(gpu_lib, pkg):
 
 @pytest.mark.parametrize("M,K,N", [(238, 10240, 2560), (5, 1024, 64), (64, 4096, 320), (130, 512, 192)])
 def test_q8_linear_split_k(gpu_lib, pkg, M, K, N):
-    # shapes whose 64 x 160 output tiles cannot fill the GPU split K over workgroups through
-    # the workspace; the last workgroup of a tile sums the fp32 partials in split order
+    # shapes whose 64-row output tiles cannot fill the GPU split K over workgroups through
+    # the workspace; a second kernel sums the fp32 partials in split order
     nbytes = pkg.kernels.q8_workspace_bytes(M, K, N)
     assert nbytes > 0, "this shape is expected to split K"
     ws = pkg.kernels.q8_workspace(M, K, N)
@@ -155,14 +168,14 @@ def test_q8_packed_scales_same_bits(gpu_lib, pkg, M, K, N):
     # the packed-scale layout is a cache: same bits as the [N, K/64] arrays, split or not
     x, q, s, b = (_t(a) for a in q8.make_q8_inputs(M, K, N, seed=N))
     sb = pkg.kernels.q8_pack_scales(s, b)
-    # layout: word (t, g, j) = b[160 t + j, g] << 16 | s[160 t + j, g], 0 past N
+    # layout: word (j, g, r) = b[32 j + r, g] << 16 | s[32 j + r, g], 0 past N
     s16, b16 = s.cpu().numpy().view(np.uint16), b.cpu().numpy().view(np.uint16)
-    T, G = -(-N // 160), K // 64
-    ref = np.zeros((T, G, 160), dtype=np.uint32)
+    T, G = -(-N // 32), K // 64
+    ref = np.zeros((T, G, 32), dtype=np.uint32)
     for t in range(T):
-        rows = np.arange(160 * t, min(160 * t + 160, N))
+        rows = np.arange(32 * t, min(32 * t + 32, N))
         ref[t, :, :len(rows)] = (b16[rows].astype(np.uint32).T << 16) | s16[rows].astype(np.uint32).T
-    assert np.array_equal(sb.cpu().numpy().view(np.uint32).reshape(T, G, 160), ref)
+    assert np.array_equal(sb.cpu().numpy().view(np.uint32).reshape(T, G, 32), ref)
     ws = pkg.kernels.q8_workspace(M, K, N)
     y_plain = pkg.kernels.q8_linear(x, q, s, b, workspace=ws)
     y_packed = pkg.kernels.q8_linear(x, q, s, b, workspace=ws, packed=sb)
@@ -196,26 +209,47 @@ def test_q8_packed_codes_same_bits(gpu_lib, pkg, M, K, N):
 
 
 def test_q8_packed_codes_layout(gpu_lib, pkg):
-    # chunk ((t S + s) 4 + w) 5 + nb, lane l: row 160 t + 32 nb + l % 32, k = 128 s + 16 w + 8 (l / 32)
-    # + 0..7, then k + 64; zeros past N and past K (N = 200: a partial second tile; 3 groups: the
-    # second step's upper half is past K)
+    # chunk ((j S + s) 4 + w), lane l: row 32 j + l % 32, k = 128 s + 16 w + 8 (l / 32) + 0..7,
+    # then k + 64; zeros past N and past K (N = 200: a partial last block; 3 groups: the second
+    # step's upper half is past K)
     N, K = 200, 192
     rng = np.random.default_rng(3)
     q = rng.integers(0, 256, (N, K), dtype=np.uint8)
     qp = pkg.kernels.q8_pack_codes(_t(q)).cpu().numpy()
-    T, S = 2, 2
-    qz = np.zeros((T * 160, S * 128), dtype=np.uint8)
+    J, S = 7, 2
+    qz = np.zeros((J * 32, S * 128), dtype=np.uint8)
     qz[:N, :K] = q
-    ref = np.zeros((T, S, 4, 5, 64, 16), dtype=np.uint8)
-    for t in range(T):
+    ref = np.zeros((J, S, 4, 64, 16), dtype=np.uint8)
+    for j in range(J):
         for st in range(S):
             for w in range(4):
-                for nb in range(5):
-                    for ln in range(64):
-                        n, k0 = 160 * t + 32 * nb + ln % 32, 128 * st + 16 * w + 8 * (ln // 32)
-                        ref[t, st, w, nb, ln, :8] = qz[n, k0:k0 + 8]
-                        ref[t, st, w, nb, ln, 8:] = qz[n, k0 + 64:k0 + 72]
+                for ln in range(64):
+                    n, k0 = 32 * j + ln % 32, 128 * st + 16 * w + 8 * (ln // 32)
+                    ref[j, st, w, ln, :8] = qz[n, k0:k0 + 8]
+                    ref[j, st, w, ln, 8:] = qz[n, k0 + 64:k0 + 72]
     assert np.array_equal(qp, ref.reshape(-1))
+
+
+@pytest.mark.parametrize("M,K,N", [(238, 2560, 7680), (238, 2560, 10240), (238, 5120, 2560), (7, 192, 320),
+                                   (65, 320, 448), (100, 64, 64)])
+def test_q8_tile_widths_same_bits(gpu_lib, pkg, M, K, N):
+    # 128- and 160-row tiles differ only in which workgroup computes an output: unsplit, the same
+    # bits (both code layouts); split, each within the oracle bars
+    K_, lib = pkg.kernels, pkg.capi.lib()
+    x, q, s, b = (_t(a) for a in q8.make_q8_inputs(M, K, N, seed=M + 3 * N))
+    sb, qp = K_.q8_pack_scales(s, b), K_.q8_pack_codes(q)
+    assert lib.q8_tile_rows(M, K, N) in (128, 160)
+    ys = {}
+    for rows in (128, 160):
+        with _tile_rows(pkg, rows):
+            assert lib.q8_tile_rows(M, K, N) == rows
+            ys[rows] = (K_.q8_linear(x, q, s, b, packed=sb), K_.q8_linear(x, q, s, b, packed=sb, codes=qp),
+                        K_.q8_linear(x, q, s, b, packed=sb, codes=qp, workspace=K_.q8_workspace(M, K, N)))
+    for y in ys[128][:2] + ys[160][:2]:
+        assert torch.equal(y.view(torch.int16), ys[160][0].view(torch.int16))
+    if M * K * N <= 238 * 2560 * 2560:
+        for rows in (128, 160):
+            _check(ys[rows][2].cpu().numpy(), *q8.make_q8_inputs(M, K, N, seed=M + 3 * N))
 
 
 @pytest.mark.parametrize("M,K,N", [(238, 2560, 10240), (50, 2560, 10240), (7, 192, 320), (100, 640, 640)])
@@ -225,7 +259,8 @@ def test_q8_swiglu_fused_same_bits(gpu_lib, pkg, M, K, N):
     K_ = pkg.kernels
     x, q, s, b = (_t(a) for a in q8.make_q8_inputs(M, K, N, seed=M + N))
     ws = K_.q8_workspace(M, K, N)
-    ref = K_.esmc_swiglu(K_.q8_linear(x, q, s, b, workspace=ws))
+    with _tile_rows(pkg, 160):  # the pair order's tile, so both calls split K alike
+        ref = K_.esmc_swiglu(K_.q8_linear(x, q, s, b, workspace=ws))
     perm = K_.swiglu_pair_rows(N, DEV)
     sbp = K_.q8_pack_scales(s[perm].contiguous(), b[perm].contiguous())
     qpp = K_.q8_pack_codes(q[perm].contiguous())
