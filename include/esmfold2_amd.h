@@ -293,8 +293,11 @@ size_t q8_linear_workspace_bytes(int M, int K, int N);
 
 /*
  * The weight rows per output tile the launch plan picks for this shape on the current
- * device: 128 when those tiles fit in one round of the GPU's CUs, else 160 when those do,
- * else the width with fewer rounds per unit of work (160 always for the SwiGLU-pair call).
+ * device, 128 or 160: the width with the lower estimated time, rounds of the GPU's CUs x
+ * 128-wide K steps per workgroup x a step's time (a 128-row step ~0.9 of a 160-row one),
+ * plus, where K is split, the fp32 partials' write and read (160 always for the SwiGLU-pair
+ * call). At M = 238: 128 for N = 7680 and for N = 2560 at K = 2560, 160 for N = 10240 and for
+ * N = 2560 at K = 5120 or 10240.
  * Either width gives the same bits when K is not split (it only changes which workgroup
  * computes an output); with a K split the split count, and so the fp32 summation order,
  * can differ. q8_set_tile_rows(128 or 160) fixes the width for every later plan of this
