@@ -148,7 +148,10 @@ __global__ __launch_bounds__(NTR) void esmc_ln_kernel(EsmcLnArgs p) {
 // roundup(D/8, 64) threads (the D/8 chunks of q and k; 320 at D = 2560, at most 512), so no
 // wave carries a second chunk. Every load is issued first (v, the q/k chunk through a
 // range-checked descriptor of the row, its LayerNorm weights) and v leaves as soon as it has
-// arrived. The LayerNorm statistics of q and k are reduced together.
+// arrived. The LayerNorm statistics of q and k are reduced together. The rotation's sines and
+// cosines are taken before the reductions, from the angle in revolutions (the hardware sine
+// of its fractional part; the angle itself is an fp32 product, as before): 5.4 -> 4.5 us at 238
+// tokens against the precise library sincos.
 constexpr int kRopeMaxThreads = 512;
 DEV float2v wg_sum2_n(float a, float b, float (*red)[kRopeMaxThreads / 64]) {
   a = row16_sum(a);
@@ -190,6 +193,17 @@ __global__ __launch_bounds__(kRopeMaxThreads) void esmc_qk_rope_kernel(EsmcRopeA
   const f32x4 w2 = *reinterpret_cast<const f32x4*>(w + HALF), w3 = *reinterpret_cast<const f32x4*>(w + HALF + 4);
   if (ev < D) st16(p.v + (((size_t)b * p.H + ev / HD) * p.L + l) * HD + ev % HD, vv);  // v: head-major
 
+  // rotation of pair i = i0 + e at position l: the angle l * base^(-2i/64) in revolutions (its
+  // fractional part), by the hardware sine and cosine; independent of the statistics, so it
+  // runs under the reductions' barriers
+  float sn[8], cs[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    float rev = (float)l * (exp2f(-(float)(2 * (i0 + e)) / HD * p.log2_base) * 0.15915494309189535f);
+    rev -= floorf(rev);
+    sn[e] = __builtin_amdgcn_sinf(rev);
+    cs[e] = __builtin_amdgcn_cosf(rev);
+  }
   float a[8], c[8], sq = 0.f, sk = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; e++) a[e] = c[e] = 0.f;
@@ -228,14 +242,9 @@ __global__ __launch_bounds__(kRopeMaxThreads) void esmc_qk_rope_kernel(EsmcRopeA
     half8 o1, o2;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-      const int i = i0 + e;
-      // rotation angle of pair i: l * base^(-2i/hd)
-      const float ang = (float)l * exp2f(-(float)(2 * i) / HD * p.log2_base);
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
       const float x1v = a[e] * rstd * wl[e], x2v = c[e] * rstd * wl[8 + e];
-      o1[e] = (half_t)(x1v * cs - x2v * sn);
-      o2[e] = (half_t)(x2v * cs + x1v * sn);
+      o1[e] = (half_t)(x1v * cs[e] - x2v * sn[e]);
+      o2[e] = (half_t)(x2v * cs[e] + x1v * sn[e]);
     }
     half_t* o = (which ? p.k : p.q) + (((size_t)b * p.H + hh) * p.L + l) * HD + i0;
     st16(o, o1);

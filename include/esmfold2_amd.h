@@ -379,7 +379,8 @@ int q8_linear_swiglu_packed_ws(const esm_half* x, const uint8_t* qp, const uint3
  * esmc_qk_rope: qkv [B*L, 3D] fp16 (the wqkv output, rows [q | k | v]); QK-LayerNorm
  *   over the full width D with weights only (:93-94), fp32 statistics; NeoX rotary
  *   embedding (mx.fast.rope traditional=False, base rope_base, positions 0..L-1,
- *   :96-97); q, k, v written head-major [B, H, L, 64] fp16. head_dim = 64, D <= 4096;
+ *   :96-97; the angle in fp32, its sine and cosine from the hardware's, on the angle in
+ *   revolutions); q, k, v written head-major [B, H, L, 64] fp16. head_dim = 64, D <= 4096;
  *   qkv, q_ln, k_ln, q, k, v 16-byte aligned.
  * esmc_attention: o = softmax(q k^T * scale, mask) v per (batch, head) (:98,
  *   mx.fast.scaled_dot_product_attention), with token i attending to j iff

@@ -42,8 +42,9 @@ def test_layer_norm(gpu_lib, pkg, D, resid, fp32_out):
         assert float((xd.double().cpu() - xr).abs().max()) <= 1e-6 * float(xr.abs().max())
 
 
-@pytest.mark.parametrize("B,L,H", [(1, 1, 2), (2, 37, 4), (1, 238, 40)])
+@pytest.mark.parametrize("B,L,H", [(1, 1, 2), (2, 37, 4), (1, 238, 40), (1, 1100, 4)])
 def test_qk_rope(gpu_lib, pkg, B, L, H):
+    # (L = 1100: the angle, up to 1099 rad, in revolutions through fp32 and the hardware sine)
     D = 64 * H
     g = _gen(L)
     qkv = torch.randn(B * L, 3 * D, generator=g).half()
