@@ -376,7 +376,7 @@ __global__ __launch_bounds__(256, NKB <= 8 ? 2 : 1) void esmc_attention_kernel(E
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m_run, mx);
     const float mref = m_new == -INFINITY ? 0.f : m_new;  // no key visible to the query yet
-    const float alpha = exp2f(m_run - mref);              // 0 on the first visible pass
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mref);  // 0 on the first visible pass
     sum *= alpha;
 #pragma unroll
     for (int db = 0; db < HD / 32; db++)
@@ -388,7 +388,7 @@ __global__ __launch_bounds__(256, NKB <= 8 ? 2 : 1) void esmc_attention_kernel(E
     for (int kb = 0; kb < KB; kb++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const float e = exp2f(sc[kb][i] - mref);
+        const float e = __builtin_amdgcn_exp2f(sc[kb][i] - mref);  // (v_exp_f32: results below 2^-126 flush)
         sum += e;
         pf[2 * kb + (i >> 3)][i & 7] = (half_t)e;
       }
@@ -432,7 +432,7 @@ __global__ __launch_bounds__(256, NKB <= 8 ? 2 : 1) void esmc_attention_kernel(E
     float den = 0.f, sc[4];
 #pragma unroll
     for (int w = 0; w < 4; w++) {
-      sc[w] = exp2f(m4[w] - M);  // 0 for a wave that saw no visible key
+      sc[w] = __builtin_amdgcn_exp2f(m4[w] - M);  // 0 for a wave that saw no visible key
       den += sc[w] * ml_s[w][1][r];
     }
     const float inv = 1.0f / den;
