@@ -213,21 +213,20 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
 }
 
 // ---- quantile of |x - y| ----------------------------------------------------------------------
-// One workgroup of QT threads. Radix selection on the bit patterns of the non-negative values
-// (their order is the value order): 3 passes of 11, 11 and 10 bits, each a histogram of the
-// candidates still matching the selected high bits, for the two ranks that bracket the
-// quantile at once; then linear interpolation between the two order statistics (the
-// definition of torch.quantile). While both ranks share their selected high bits (always in
-// the first pass, and in most later ones since the ranks are adjacent) one histogram serves
-// both. Up to QT * QC values the patterns stay in registers after the first pass (thread tid
-// holds values tid + QT j), so only one pass reads memory; beyond that every pass scans x and
-// y in chunks of QT * QU values. Loads go through range-checked buffer descriptors with no
-// branch around them, so a thread's loads are in flight together.
+// Beyond the register-held sizes (abs_diff_quantile_regs_kernel below): one workgroup of QT
+// threads. Radix selection on the bit patterns of the non-negative values (their order is the
+// value order): 3 passes of 11, 11 and 10 bits, each a histogram of the candidates still
+// matching the selected high bits, for the two ranks that bracket the quantile at once; then
+// linear interpolation between the two order statistics (the definition of torch.quantile).
+// While both ranks share their selected high bits (always in the first pass, and in most later
+// ones since the ranks are adjacent) one histogram serves both. Every pass scans x and y in
+// chunks of QT * QU values through range-checked buffer descriptors with no branch around the
+// loads, so a thread's loads are in flight together.
 constexpr int QT = 1024;
 __global__ __launch_bounds__(QT) void abs_diff_quantile_kernel(const float* __restrict__ x,
                                                                const float* __restrict__ y, size_t n, float q,
                                                                float* __restrict__ out) {
-  constexpr int NBIN = 2048, BPT = NBIN / QT, NWV = QT / 64, QU = 8, QC = 56;
+  constexpr int NBIN = 2048, BPT = NBIN / QT, NWV = QT / 64, QU = 8;
   constexpr uint32_t kNone = 0xffffffffu;  // an index past n: no prefix of a |value| matches it
   __shared__ uint32_t hist[2][NBIN];
   __shared__ uint32_t sel[2];
@@ -258,8 +257,6 @@ __global__ __launch_bounds__(QT) void abs_diff_quantile_kernel(const float* __re
   auto pattern = [&](uint32_t xb, uint32_t yb, uint32_t i, size_t cnt) {
     return __float_as_uint(fabsf(__uint_as_float(xb) - __uint_as_float(yb))) | (i < cnt ? 0u : kNone);
   };
-  const bool cached = n <= (size_t)QT * QC;
-  uint32_t uc[QC];
   uint32_t prefix[2] = {0u, 0u}, mask = 0u;
   const int shifts[3] = {21, 10, 0}, widths[3] = {11, 11, 10};
 #pragma unroll
@@ -274,40 +271,18 @@ __global__ __launch_bounds__(QT) void abs_diff_quantile_kernel(const float* __re
     };
     for (int k = tid; k < 2 * NBIN; k += QT) (&hist[0][0])[k] = 0u;
     __syncthreads();
-    if (cached) {
-      if (ps == 0) {
-        // all of x in flight, then y in groups of 8
-        rsrc_t rx, ry;
-        chunk(0, n, rx, ry);
+    for (size_t c0 = 0; c0 < n; c0 += (size_t)QT * QU) {
+      const size_t cnt = n - c0 < (size_t)QT * QU ? n - c0 : (size_t)QT * QU;
+      rsrc_t rx, ry;
+      chunk(c0, cnt, rx, ry);
+      uint32_t xb[QU], yb[QU];
 #pragma unroll
-        for (int j = 0; j < QC; j++) uc[j] = ld(rx, j);
-#pragma unroll
-        for (int g = 0; g < QC / 8; g++) {
-          uint32_t yb[8];
-#pragma unroll
-          for (int j = 0; j < 8; j++) yb[j] = ld(ry, 8 * g + j);
-#pragma unroll
-          for (int j = 0; j < 8; j++)
-            uc[8 * g + j] = pattern(uc[8 * g + j], yb[j], (uint32_t)(tid + QT * (8 * g + j)), n);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+      for (int j = 0; j < QU; j++) {
+        xb[j] = ld(rx, j);
+        yb[j] = ld(ry, j);
       }
 #pragma unroll
-      for (int j = 0; j < QC; j++) count(uc[j]);
-    } else {
-      for (size_t c0 = 0; c0 < n; c0 += (size_t)QT * QU) {
-        const size_t cnt = n - c0 < (size_t)QT * QU ? n - c0 : (size_t)QT * QU;
-        rsrc_t rx, ry;
-        chunk(c0, cnt, rx, ry);
-        uint32_t xb[QU], yb[QU];
-#pragma unroll
-        for (int j = 0; j < QU; j++) {
-          xb[j] = ld(rx, j);
-          yb[j] = ld(ry, j);
-        }
-#pragma unroll
-        for (int j = 0; j < QU; j++) count(pattern(xb[j], yb[j], (uint32_t)(tid + QT * j), cnt));
-      }
+      for (int j = 0; j < QU; j++) count(pattern(xb[j], yb[j], (uint32_t)(tid + QT * j), cnt));
     }
     __syncthreads();
     // Each rank's bin: thread tid owns bins BPT tid .. BPT tid + BPT - 1; an exclusive scan of
@@ -365,6 +340,201 @@ __global__ __launch_bounds__(QT) void abs_diff_quantile_kernel(const float* __re
   }
 }
 
+// Up to QR * QCR = 57,344 values (every pair grid up to L = 239): the same order statistics in
+// two passes, the values held in registers (512 threads of 112 values: the 1024-thread form has
+// 128 registers per thread, which 56 values and the scans overflow). Pass 0 counts the 15 bits
+// under the (zero) sign bit, bits 30..16, in 32,768 bins (128 KB of LDS); a workgroup-wide scan
+// gives the bins b0, b1 of the two ranks. When b0 == b1 (nearly always: the ranks are adjacent)
+// pass 1 counts the low 16 bits of that bin's values in 65,536 bins of 16-bit counters packed two
+// to a word (no count can exceed n < 2^16), and a second scan gives both ranks' low bits. When
+// b0 != b1 the lower rank is the largest value of b0 and the upper the smallest of b1: one
+// maximum and one minimum, reduced per wave before a single LDS atomic each.
+constexpr int QR = 512, QCR = 112;
+__global__ __launch_bounds__(QR) void abs_diff_quantile_regs_kernel(const float* __restrict__ x,
+                                                                    const float* __restrict__ y, uint32_t n,
+                                                                    float q, float* __restrict__ out) {
+  constexpr int NWV = QR / 64;
+  constexpr int NW0 = 1 << 15;             // words of the histogram: pass-0 bins, or pass 1's packed pairs
+  constexpr int WPT = NW0 / QR;            // words per thread in the scans (64)
+  constexpr int CPT = WPT / 4;             // their 16-byte chunks (16)
+  constexpr uint32_t kNone = 0xffffffffu;  // past n: its top bits (0xffff) match no bin
+  static_assert(CPT == 16 && QCR % 8 == 0, "16 chunks per thread; y in groups of 8");
+  __shared__ __align__(16) uint32_t h[NW0];
+  __shared__ uint32_t wsum[NWV];
+  __shared__ uint32_t sel[2], rk_s[2], mm[2];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const double pos = (double)q * (double)(n - 1);
+  const uint32_t lo = (uint32_t)pos, hi = lo + 1 < n ? lo + 1 : lo;
+  const float frac = (float)(pos - (double)lo);
+  const int nj = (int)(4 * ((n / 4 + QR - 1) / QR));  // slots j < nj can hold values of the pieces
+
+  auto zero_hist = [&]() {  // one address register stepped through (unrolled, the offsets past 64 KB each need one)
+#pragma unroll 1
+    for (int k = tid; k < NW0 / 4; k += QR) reinterpret_cast<uint4*>(h)[k] = make_uint4(0u, 0u, 0u, 0u);
+  };
+  // Both ranks' bins in the histogram h (PK: two 16-bit counts per word, the even bin low).
+  // Thread tid owns words WPT tid .. WPT tid + WPT - 1; it sums them in a lane-rotated order (of
+  // 16-byte chunks: the 8 lanes one read serves hit 8 distinct 4-bank groups), a workgroup scan
+  // of the sums gives the counts before each thread's words, and the thread whose words hold a
+  // rank finds the chunk, then the word and the bin. sel[t] = the bin, rk_s[t] = the rank within it.
+  auto select = [&](auto packed, uint32_t r0, uint32_t r1) {
+    constexpr bool PK = decltype(packed)::value;
+    auto wcount = [](uint32_t w) { return PK ? (w & 0xffffu) + (w >> 16) : w; };
+    uint32_t c = 0;
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      const uint4 w = *reinterpret_cast<const uint4*>(&h[WPT * tid + 4 * ((k + lane) & (CPT - 1))]);
+      c += wcount(w.x) + wcount(w.y) + wcount(w.z) + wcount(w.w);
+    }
+    uint32_t inc = c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_up(inc, off);
+      if (lane >= off) inc += o;
+    }
+    if (lane == 63) wsum[wv] = inc;
+    __syncthreads();
+    uint32_t before = inc - c;
+    for (int w = 0; w < wv; w++) before += wsum[w];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const uint32_t r = t ? r1 : r0;
+      if (r >= before && r < before + c) {  // exactly one thread per rank
+        uint4 ch[CPT];  // all of the thread's chunks in flight
+#pragma unroll
+        for (int k = 0; k < CPT; k++) ch[k] = *reinterpret_cast<const uint4*>(&h[WPT * tid + 4 * k]);
+        uint32_t acc = before;
+        int kc = CPT - 1;
+#pragma unroll
+        for (int k = 0; k < CPT - 1; k++) {
+          const uint32_t cs = wcount(ch[k].x) + wcount(ch[k].y) + wcount(ch[k].z) + wcount(ch[k].w);
+          if (kc == CPT - 1) {
+            if (r < acc + cs)
+              kc = k;
+            else
+              acc += cs;
+          }
+        }
+        uint4 cw = ch[0];
+#pragma unroll
+        for (int k = 1; k < CPT; k++)
+          if (kc == k) cw = ch[k];
+        const uint32_t wd[4] = {cw.x, cw.y, cw.z, cw.w};
+        int bin = -1;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+          for (int e = 0; e < (PK ? 2 : 1); e++) {
+            const uint32_t cnt = PK ? (e ? wd[k] >> 16 : wd[k] & 0xffffu) : wd[k];
+            if (bin < 0) {
+              if (r < acc + cnt)
+                bin = (PK ? 2 : 1) * (WPT * tid + 4 * kc + k) + e;
+              else
+                acc += cnt;
+            }
+          }
+        sel[t] = (uint32_t)bin;
+        rk_s[t] = r - acc;
+      }
+    }
+    __syncthreads();
+  };
+
+  zero_hist();
+  // Loads as 16-byte pieces (a quarter of the load instructions: their issue, not the bytes,
+  // bounds a single workgroup's reads): thread tid holds values 4 (tid + QR j) .. +3, j < QCR / 4,
+  // of the first n4 = n - n % 4 (every piece wholly inside or wholly past that range), and
+  // threads 0 .. n % 4 - 1 hold the tail value n4 + tid in ut (kNone elsewhere). All of x in
+  // flight, then y two pieces at a time; range-checked descriptors, no branch around the loads.
+  uint32_t uc[QCR], ut;
+  {
+    const uint32_t n4 = n & ~3u;
+    const rsrc_t rx = make_rsrc_n(x, n4 * 4u), ry = make_rsrc_n(y ? y : x, y ? n4 * 4u : 0u);
+#pragma unroll
+    for (int j = 0; j < QCR / 4; j++) {
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, tid * 16, QR * 16 * j, 0));
+#pragma unroll
+      for (int e = 0; e < 4; e++) uc[4 * j + e] = v[e];
+    }
+#pragma unroll
+    for (int g = 0; g < QCR / 8; g++) {
+      u32x4 yb[2];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; h2++)
+        yb[h2] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ry, tid * 16, QR * 16 * (2 * g + h2), 0));
+#pragma unroll
+      for (int h2 = 0; h2 < 2; h2++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int j = 4 * (2 * g + h2) + e;
+          const uint32_t i = 4u * (uint32_t)(tid + QR * (2 * g + h2)) + e;
+          uc[j] = __float_as_uint(fabsf(__uint_as_float(uc[j]) - __uint_as_float(yb[h2][e]))) | (i < n4 ? 0u : kNone);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const rsrc_t tx = make_rsrc_n(x, n * 4u), ty = make_rsrc_n(y ? y : x, y ? n * 4u : 0u);
+    const bool tail = (uint32_t)tid < n - n4;
+    const uint32_t toff = tail ? (n4 + (uint32_t)tid) * 4u : kOOB;
+    const uint32_t xt = __builtin_amdgcn_raw_buffer_load_b32(tx, (int)toff, 0, 0);
+    const uint32_t yt = __builtin_amdgcn_raw_buffer_load_b32(ty, (int)toff, 0, 0);
+    ut = __float_as_uint(fabsf(__uint_as_float(xt) - __uint_as_float(yt))) | (tail ? 0u : kNone);
+  }
+  __syncthreads();  // the histogram is zero
+#pragma unroll
+  for (int j = 0; j < QCR; j++)
+    if (j < nj && uc[j] != kNone) atomicAdd(&h[uc[j] >> 16], 1u);
+  if (ut != kNone) atomicAdd(&h[ut >> 16], 1u);
+  __syncthreads();
+  select(std::false_type{}, lo, hi);
+  const uint32_t b0 = sel[0], b1 = sel[1];
+  uint32_t d0, d1;
+  if (b0 == b1) {  // block-uniform
+    const uint32_t r0 = rk_s[0], r1 = rk_s[1];
+    __syncthreads();  // every thread has read sel and rk_s
+    zero_hist();
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j <= QCR; j++) {  // j == QCR: the tail value
+      const uint32_t u = j < QCR ? uc[j] : ut;
+      if ((j < nj || j == QCR) && (u >> 16) == b0) atomicAdd(&h[(u & 0xffffu) >> 1], 1u << ((u & 1u) << 4));
+    }
+    __syncthreads();
+    select(std::true_type{}, r0, r1);
+    d0 = sel[0];
+    d1 = sel[1];
+  } else {
+    if (tid == 0) {
+      mm[0] = 0u;
+      mm[1] = 0xffffu;
+    }
+    uint32_t mx = 0u, mn = 0xffffu;
+#pragma unroll
+    for (int j = 0; j <= QCR; j++) {  // j == QCR: the tail value
+      const uint32_t u = j < QCR ? uc[j] : ut;
+      const bool on = j < nj || j == QCR;
+      if (on && (u >> 16) == b0) mx = max(mx, u & 0xffffu);
+      if (on && (u >> 16) == b1) mn = min(mn, u & 0xffffu);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+      mn = min(mn, (uint32_t)__shfl_xor((int)mn, off));
+    }
+    __syncthreads();  // mm initialised
+    if (lane == 0) {
+      atomicMax(&mm[0], mx);
+      atomicMin(&mm[1], mn);
+    }
+    __syncthreads();
+    d0 = mm[0];
+    d1 = mm[1];
+  }
+  if (tid == 0) {
+    const float a = __uint_as_float((b0 << 16) | d0), b = __uint_as_float((b1 << 16) | d1);
+    out[0] = a + frac * (b - a);
+  }
+}
+
 hipError_t launch_parcae_step(const ParcaeArgs& a, int grid, hipStream_t s) {
   if (a.C == 128)
     ESM_LAUNCH(parcae_step_kernel<128>, dim3(grid), dim3(256), 0, s, a);
@@ -390,7 +560,10 @@ hipError_t launch_expected_distance(const DistoArgs& a, int grid, hipStream_t s)
 }
 
 hipError_t launch_abs_diff_quantile(const float* x, const float* y, size_t n, float q, float* out, hipStream_t s) {
-  ESM_LAUNCH(abs_diff_quantile_kernel, dim3(1), dim3(QT), 0, s, x, y, n, q, out);
+  if (n <= (size_t)QR * QCR)
+    ESM_LAUNCH(abs_diff_quantile_regs_kernel, dim3(1), dim3(QR), 0, s, x, y, (uint32_t)n, q, out);
+  else
+    ESM_LAUNCH(abs_diff_quantile_kernel, dim3(1), dim3(QT), 0, s, x, y, n, q, out);
   return hipGetLastError();
 }
 

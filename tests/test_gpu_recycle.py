@@ -51,10 +51,11 @@ def test_expected_distance(gpu_lib, pkg, L, nbins):
     assert torch.equal(ed, ed.transpose(1, 2))
 
 
-@pytest.mark.parametrize("n", [1, 2, 3, 1000, 56644, 65536, 65537, 300000])
+@pytest.mark.parametrize("n", [1, 2, 3, 1000, 1001, 56644, 57343, 57344, 57345, 65536, 65537, 300000])
 @pytest.mark.parametrize("q", [0.0, 0.5, 0.95, 1.0])
 def test_abs_diff_quantile(gpu_lib, pkg, n, q):
-    """Against torch.quantile, with ties, at the endpoints and across 2^16 values."""
+    """Against torch.quantile, with ties, at the endpoints, across the largest size held in
+    registers (57,344; n % 4 != 0 takes the tail loads) and across 2^16 values."""
     g = torch.Generator().manual_seed(n)
     x = torch.randn(n, generator=g) * 3
     y = torch.randn(n, generator=g) * 3
@@ -66,6 +67,29 @@ def test_abs_diff_quantile(gpu_lib, pkg, n, q):
     assert abs(got - ref) <= 1e-6 * max(1.0, abs(ref))
     got1 = float(pkg.kernels.abs_diff_quantile(x.to(DEV), None, q).item())
     assert abs(got1 - float(torch.quantile(x.abs().double(), q))) <= 1e-6 * max(1.0, float(x.abs().max()))
+
+
+@pytest.mark.parametrize("n", [1000, 57344, 60000])
+def test_abs_diff_quantile_ranks_in_two_bins(gpu_lib, pkg, n):
+    """The two order statistics around the quantile in different histogram bins (1.00x and
+    1.5x differ in their top 16 bits), so the lower is the largest of one bin and the upper the
+    smallest of the next; interpolated halfway, at the largest size held in registers and past it."""
+    g = torch.Generator().manual_seed(7)
+    k = n - n // 20
+    x = torch.empty(n)
+    x[:k] = 1.0 + torch.rand(k, generator=g) * 0.007  # all in the bin of 1.0 (top 16 bits 0x3f80)
+    x[k:] = 1.5 + torch.rand(n - k, generator=g) * 0.4
+    x = x[torch.randperm(n, generator=g)]
+    # pos = k - 1/2: between the k-th smallest (1.00x) and the next (1.5x); q as the kernel
+    # receives it (fp32), since here the interpolation weight moves the result by ~0.5 per unit
+    q = float(torch.tensor((k - 0.5) / (n - 1), dtype=torch.float32))
+    got = float(pkg.kernels.abs_diff_quantile(x.to(DEV), None, q).item())
+    ref = float(torch.quantile(x.double(), q))
+    assert abs(got - ref) <= 1e-6 * abs(ref)
+    y = torch.rand(n, generator=g) * 0.001
+    got = float(pkg.kernels.abs_diff_quantile((x + y).to(DEV), y.to(DEV), q).item())
+    ref = float(torch.quantile(((x + y) - y).abs().double(), q))
+    assert abs(got - ref) <= 1e-6 * abs(ref)
 
 
 @pytest.mark.parametrize("n", [4096, 65536, 70000])
