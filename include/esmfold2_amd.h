@@ -422,7 +422,9 @@ int esmc_swiglu(const esm_half* x12, esm_half* y, int M, int F, void* stream);
  * abs_diff_quantile: out[0] = the q-th quantile of |x - y| (y NULL: of |x|) over n values,
  *   linear interpolation between the two nearest order statistics, as torch.quantile
  *   (the exit signal: var_6b_mlx_loop.py:79-85 with q = 0.95, var_adaptive_loops.py:116).
- *   Exact (order statistics by radix selection). x, y [n] fp32; out one fp32.
+ *   Exact (order statistics by radix selection). x, y [n] fp32; out one fp32. A NaN difference
+ *   orders above +inf, as the sort of the MLX loop's p95 (var_6b_mlx_loop.py:78-84) orders it
+ *   (torch.quantile would return NaN instead).
  */
 int parcae_step(const float* z, const float* z_init, const float* refined, const float* ln_w, const float* ln_b,
                 float eps, const float* a, const esm_half* b_mat, float* z_out, int B, int L, int C, void* stream);
