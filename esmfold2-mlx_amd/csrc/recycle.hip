@@ -341,24 +341,25 @@ __global__ __launch_bounds__(QT) void abs_diff_quantile_kernel(const float* __re
 }
 
 // Up to QR * QCR = 57,344 values (every pair grid up to L = 239): the same order statistics in
-// two passes, the values held in registers (512 threads of 112 values: the 1024-thread form has
-// 128 registers per thread, which 56 values and the scans overflow). Pass 0 counts the 15 bits
+// two passes, the values held in registers (1024 threads of 56 values: sixteen waves hide the
+// scans' and the atomics' latency better than eight of 112, 17.6 against 21.5 us at L = 238,
+// within the 128 registers a thread has at that size). Pass 0 counts the 15 bits
 // under the (zero) sign bit, bits 30..16, in 32,768 bins (128 KB of LDS); a workgroup-wide scan
 // gives the bins b0, b1 of the two ranks. When b0 == b1 (nearly always: the ranks are adjacent)
 // pass 1 counts the low 16 bits of that bin's values in 65,536 bins of 16-bit counters packed two
 // to a word (no count can exceed n < 2^16), and a second scan gives both ranks' low bits. When
 // b0 != b1 the lower rank is the largest value of b0 and the upper the smallest of b1: one
 // maximum and one minimum, reduced per wave before a single LDS atomic each.
-constexpr int QR = 512, QCR = 112;
+constexpr int QR = 1024, QCR = 56;
 __global__ __launch_bounds__(QR) void abs_diff_quantile_regs_kernel(const float* __restrict__ x,
                                                                     const float* __restrict__ y, uint32_t n,
                                                                     float q, float* __restrict__ out) {
   constexpr int NWV = QR / 64;
   constexpr int NW0 = 1 << 15;             // words of the histogram: pass-0 bins, or pass 1's packed pairs
-  constexpr int WPT = NW0 / QR;            // words per thread in the scans (64)
-  constexpr int CPT = WPT / 4;             // their 16-byte chunks (16)
+  constexpr int WPT = NW0 / QR;            // words per thread in the scans
+  constexpr int CPT = WPT / 4;             // their 16-byte chunks
   constexpr uint32_t kNone = 0xffffffffu;  // past n: its top bits (0xffff) match no bin
-  static_assert(CPT == 16 && QCR % 8 == 0, "16 chunks per thread; y in groups of 8");
+  static_assert((CPT & (CPT - 1)) == 0 && QCR % 8 == 0, "a power-of-two chunk count; y in groups of 8");
   __shared__ __align__(16) uint32_t h[NW0];
   __shared__ uint32_t wsum[NWV];
   __shared__ uint32_t sel[2], rk_s[2], mm[2];
