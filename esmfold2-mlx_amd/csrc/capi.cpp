@@ -3,6 +3,7 @@
 // memory; every launch goes on the caller's stream.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -838,8 +839,10 @@ int distogram_expected_distance(const float* r, const esm_half* w, const float* 
   if (!r || !w || !bias || !centers || !ed) return fail(ESM_ERR_NULL, "distogram_expected_distance: NULL pointer");
   if (!aligned16(r) || !aligned16(w)) return fail(ESM_ERR_ALIGN, "distogram_expected_distance: r, w must be 16-byte aligned");
   esm::DistoArgs args{r, H(w), bias, centers, ed, B, L, nbins, C};
-  const long long tiles = (long long)B * L * ((L + 127) / 128);
-  const int grid = (int)(tiles < 4LL * cu_count() ? tiles : 4LL * cu_count());
+  long long units = 0;  // one wave per 32 pairs j >= i of a row, 4 waves per workgroup
+  for (int I = 0, JT = (L + 31) / 32; I < JT; I++) units += (long long)std::min(32, L - 32 * I) * (JT - I);
+  const long long blocks = (B * units + 3) / 4;
+  const int grid = (int)(blocks < 4LL * cu_count() ? blocks : 4LL * cu_count());
   return hip_status(esm::launch_expected_distance(args, grid, (hipStream_t)stream), "distogram_expected_distance launch");
 }
 

@@ -123,7 +123,12 @@ __global__ __launch_bounds__(256, 1) void parcae_step_kernel(ParcaeArgs p) {
 }
 
 // ---- expected distance ----------------------------------------------------------------------
-// One wave per 32 pairs (b, i, j0 .. j0+31); 4 waves per workgroup. The B operand is
+// The head is symmetric in (i, j): s[i,j] = r[i,j] + r[j,i] is the same fp32 sum both ways
+// round, so only pairs j >= i are computed and each result is written to ed[i,j] and ed[j,i];
+// every cell of r is then read from HBM once (both orders per pair: r[i,j] and r[j,i]).
+// One wave per 32 pairs (b, i, j0 .. j0+31) with j0 = 32 * jt over the tiles jt >= i / 32;
+// lanes with j < i (the diagonal tile) re-read the cell (i, i) and write nothing. Waves take
+// units independently (no barrier after the set-up). The B operand is
 // s[cell][c] = r[b,i,j,c] + r[b,j,i,c] rounded to fp16, read straight into fragments
 // (column = pair, k = channel); A = the head's weight rows (bins), held in registers, or
 // for the widest heads (128 bins at 256 channels: 256 registers of fragments) read from an
@@ -158,14 +163,24 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
   __syncthreads();
 
   const int L = p.L;
-  const int jt = (L + 127) / 128;  // 128-pair tiles per (b, i)
-  for (int t = blockIdx.x; t < p.B * L * jt; t += gridDim.x) {
-    const int bi = t / jt, j0 = (t - bi * jt) * 128 + 32 * wave;
-    const int b = bi / L, i = bi - b * L;
-    const int j = j0 + r;
-    const bool live = j < L;
-    const float* rij = p.r + (((size_t)b * L + i) * L + (live ? j : 0)) * CC;
-    const float* rji = p.r + (((size_t)b * L + (live ? j : 0)) * L + i) * CC;
+  const int JT = (L + 31) / 32;  // 32-pair tiles per row
+  // units per batch: rows of block I (32 rows, the last one L - 32 I) hold JT - I tiles each
+  int per_b = 0;
+  for (int I = 0; I < JT; I++) per_b += min(32, L - 32 * I) * (JT - I);
+  const int U = p.B * per_b;
+  for (int u = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(wave); u < U; u += gridDim.x * 4) {
+    const int b = u / per_b;
+    int rem = u - b * per_b, I = 0;
+    while (rem >= 32 * (JT - I)) {
+      rem -= 32 * (JT - I);
+      I++;
+    }
+    const int row = rem / (JT - I), jt = I + (rem - row * (JT - I));
+    const int i = 32 * I + row, j = 32 * jt + r;
+    const bool live = j >= i && j < L;
+    const int jj = live ? j : i;
+    const float* rij = p.r + (((size_t)b * L + i) * L + jj) * CC;
+    const float* rji = p.r + (((size_t)b * L + jj) * L + i) * CC;
     f32x16 d[NBB];
 #pragma unroll
     for (int bb = 0; bb < NBB; bb++)
@@ -208,7 +223,11 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
       }
     se += __shfl_xor(se, 32);
     sc += __shfl_xor(sc, 32);
-    if (live && h == 0) p.ed[((size_t)b * L + i) * L + j] = sc / se;
+    if (live && h == 0) {
+      const float v = sc / se;
+      p.ed[((size_t)b * L + i) * L + j] = v;
+      if (j != i) p.ed[((size_t)b * L + j) * L + i] = v;
+    }
   }
 }
 
