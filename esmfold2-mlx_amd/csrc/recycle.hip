@@ -127,22 +127,28 @@ __global__ __launch_bounds__(256, 1) void parcae_step_kernel(ParcaeArgs p) {
 // round, so only pairs j >= i are computed and each result is written to ed[i,j] and ed[j,i];
 // every cell of r is then read from HBM once (both orders per pair: r[i,j] and r[j,i]).
 // One wave per 32 pairs (b, i, j0 .. j0+31) with j0 = 32 * jt over the tiles jt >= i / 32;
-// lanes with j < i (the diagonal tile) re-read the cell (i, i) and write nothing. Waves take
-// units independently (no barrier after the set-up). The B operand is
-// s[cell][c] = r[b,i,j,c] + r[b,j,i,c] rounded to fp16, read straight into fragments
-// (column = pair, k = channel); A = the head's weight rows (bins), held in registers, or
-// for the widest heads (128 bins at 256 channels: 256 registers of fragments) read from an
-// LDS copy per k-step. A lane then holds its pair's logits for 16 bins per 32-bin block: the
+// lanes for j < i (the diagonal tile) re-read the cell (i, i) and write nothing. Waves take
+// units independently (no workgroup barrier after the set-up).
+// Loads: each instruction reads whole cells (64 lanes x 16 bytes = 256 / CC cells), r[i,j]
+// and r[j,i] in the same lane layout, so the fp32 sum is formed in registers, rounded to fp16
+// and stored to the wave's LDS rows s[cell][c]. The MFMA's B operand (column = pair, k =
+// channel) is read from there; A = the head's weight rows (bins), held in registers, or for
+// the widest heads (128 bins at 256 channels: 256 registers of fragments) read from an LDS
+// copy per k-step. A lane then holds its pair's logits for 16 bins per 32-bin block: the
 // softmax over bins is a register reduction plus one exchange between the lane halves.
 // Bias and centres come from LDS.
 template <int NBB, int CC>  // 32-bin blocks, channels
 __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) {
   constexpr int NB = 32 * NBB;
   constexpr bool WLDS = NBB * CC > 512;   // fragments from LDS instead of registers
-  constexpr int WS = CC + 8;              // LDS row stride (halfs) of the weight copy
+  constexpr int WS = CC + 8;              // LDS row stride (halfs) of the weight copy and the pair rows
+  constexpr int LPC = CC / 4;             // lanes per cell in a load instruction
+  constexpr int CPI = 64 / LPC;           // cells per load instruction
+  constexpr int QB = CC == 128 ? 16 : 8;  // load instructions in flight per array
   __shared__ float bias_s[NB], cent_s[NB];
   __shared__ __align__(16) half_t w_s[WLDS ? NB * WS : 8];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ __align__(16) half_t s_s[4][32 * WS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
   for (int k = tid; k < NB; k += 256) {
     bias_s[k] = p.bias[k];
@@ -162,13 +168,15 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
   }
   __syncthreads();
 
+  half_t* sw = s_s[wave];
   const int L = p.L;
   const int JT = (L + 31) / 32;  // 32-pair tiles per row
   // units per batch: rows of block I (32 rows, the last one L - 32 I) hold JT - I tiles each
   int per_b = 0;
   for (int I = 0; I < JT; I++) per_b += min(32, L - 32 * I) * (JT - I);
   const int U = p.B * per_b;
-  for (int u = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(wave); u < U; u += gridDim.x * 4) {
+  const int lc = lane / LPC, f = 4 * (lane - lc * LPC);  // cell within an instruction, channel
+  for (int u = blockIdx.x * 4 + wave; u < U; u += gridDim.x * 4) {
     const int b = u / per_b;
     int rem = u - b * per_b, I = 0;
     while (rem >= 32 * (JT - I)) {
@@ -176,11 +184,30 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
       I++;
     }
     const int row = rem / (JT - I), jt = I + (rem - row * (JT - I));
-    const int i = 32 * I + row, j = 32 * jt + r;
-    const bool live = j >= i && j < L;
-    const int jj = live ? j : i;
-    const float* rij = p.r + (((size_t)b * L + i) * L + jj) * CC;
-    const float* rji = p.r + (((size_t)b * L + jj) * L + i) * CC;
+    const int i = 32 * I + row;
+    const float* ri = p.r + ((size_t)b * L + i) * L * CC;  // row i
+    const float* rc = p.r + (size_t)b * L * L * CC + (size_t)i * CC;  // column i
+#pragma unroll
+    for (int q0 = 0; q0 < 32 / CPI; q0 += QB) {
+      f32x4 x[QB], y[QB];
+#pragma unroll
+      for (int q = 0; q < QB; q++) {
+        const int j = 32 * jt + CPI * (q0 + q) + lc;
+        const int jj = j >= i && j < L ? j : i;
+        x[q] = *reinterpret_cast<const f32x4*>(ri + (size_t)jj * CC + f);
+        y[q] = *reinterpret_cast<const f32x4*>(rc + (size_t)jj * L * CC + f);
+      }
+#pragma unroll
+      for (int q = 0; q < QB; q++) {
+        half4 v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = (half_t)(x[q][e] + y[q][e]);
+        *reinterpret_cast<half4*>(&sw[(CPI * (q0 + q) + lc) * WS + f]) = v;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     f32x16 d[NBB];
 #pragma unroll
     for (int bb = 0; bb < NBB; bb++)
@@ -189,20 +216,17 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
 #pragma unroll
     for (int ks = 0; ks < CC / 16; ks++) {
       const int c0 = 16 * ks + 8 * h;
-      half8 s;
-#pragma unroll
-      for (int hh = 0; hh < 2; hh++) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(rij + c0 + 4 * hh);
-        const f32x4 y = *reinterpret_cast<const f32x4*>(rji + c0 + 4 * hh);
-#pragma unroll
-        for (int e = 0; e < 4; e++) s[4 * hh + e] = (half_t)(x[e] + y[e]);
-      }
+      const half8 sv = ld16(&sw[r * WS + c0]);
 #pragma unroll
       for (int bb = 0; bb < NBB; bb++) {
         const half8 w = WLDS ? ld16(&w_s[(32 * bb + r) * WS + c0]) : wa[WLDS ? 0 : bb][WLDS ? 0 : ks];
-        d[bb] = mfma32(w, s, d[bb]);
+        d[bb] = mfma32(w, sv, d[bb]);
       }
     }
+    // the next unit's stores to sw come after every lane's fragment reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float mx = -INFINITY;
 #pragma unroll
     for (int bb = 0; bb < NBB; bb++)
@@ -223,7 +247,8 @@ __global__ __launch_bounds__(256, 1) void expected_distance_kernel(DistoArgs p) 
       }
     se += __shfl_xor(se, 32);
     sc += __shfl_xor(sc, 32);
-    if (live && h == 0) {
+    const int j = 32 * jt + r;
+    if (j >= i && j < L && h == 0) {
       const float v = sc / se;
       p.ed[((size_t)b * L + i) * L + j] = v;
       if (j != i) p.ed[((size_t)b * L + j) * L + i] = v;
