@@ -419,6 +419,8 @@ int esmc_swiglu(const esm_half* x12, esm_half* y, int M, int F, void* stream);
  *   residue axes. r [B, L, L, C] fp32 (the readout or the coda output); w [nbins, C] fp16
  *   (the head's weight); bias, centers [nbins] fp32; ed [B, L, L] fp32. The pair sums are
  *   rounded to fp16 for the MFMA; logits and softmax in fp32. C = 128 or 256, nbins 64 or 128.
+ *   ed is exactly symmetric: each pair j >= i is computed once and stored to ed[i,j] and
+ *   ed[j,i] (r[i,j] + r[j,i] is the same fp32 sum either way round), so r is read once.
  * abs_diff_quantile: out[0] = the q-th quantile of |x - y| (y NULL: of |x|) over n values,
  *   linear interpolation between the two nearest order statistics, as torch.quantile
  *   (the exit signal: var_6b_mlx_loop.py:79-85 with q = 0.95, var_adaptive_loops.py:116).
