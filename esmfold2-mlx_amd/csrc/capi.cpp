@@ -824,7 +824,9 @@ int parcae_step(const float* z, const float* z_init, const float* refined, const
     return fail(ESM_ERR_ALIGN, "parcae_step: z, z_init, refined, z_out, b_mat must be 16-byte aligned");
   const size_t ntiles = (ncells + 31) / 32;
   esm::ParcaeArgs args{z, z_init, refined, ln_w, ln_b, eps, a, H(b_mat), z_out, ncells, (int)ntiles, C};
-  const int grid = (int)(ntiles < (size_t)cu_count() ? ntiles : cu_count());
+  // two workgroups per CU at C = 128 (20.1 against 21.7 us at L=238); at C = 256 one (45 us; two: 50)
+  const size_t cap = (size_t)cu_count() * (C == 128 ? 2 : 1);
+  const int grid = (int)(ntiles < cap ? ntiles : cap);
   return hip_status(esm::launch_parcae_step(args, grid, (hipStream_t)stream), "parcae_step launch");
 }
 
