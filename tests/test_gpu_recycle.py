@@ -51,6 +51,23 @@ def test_expected_distance(gpu_lib, pkg, L, nbins):
     assert torch.equal(ed, ed.transpose(1, 2))
 
 
+@pytest.mark.parametrize("B,L,C,nbins", [(2, 257, 128, 64), (2, 97, 256, 128), (1, 257, 256, 64), (3, 32, 128, 128)])
+def test_expected_distance_tiles_and_batches(gpu_lib, pkg, B, L, C, nbins):
+    """Pairs j >= i in 32-pair tiles: a partial last row block (L = 257, 97), several batches (the
+    unit index crossing b), both widths and both bin counts (128 bins at C = 256 reads the weight
+    rows from LDS). The result is exactly symmetric and matches the fp16-rounded pair sums."""
+    g = torch.Generator().manual_seed(B * 1000 + L + C + nbins)
+    r = torch.randn(B, L, L, C, generator=g)
+    w = (torch.randn(nbins, C, generator=g) * 0.05).half()
+    b = torch.randn(nbins, generator=g)
+    c = orc.centers_6b() if nbins == 64 else orc.centers_experimental()
+    ed = pkg.kernels.expected_distance(r.to(DEV), w.to(DEV), b.to(DEV), c.float().to(DEV)).double().cpu()
+    assert torch.equal(ed, ed.transpose(1, 2))
+    s16 = (r + r.transpose(1, 2)).half().double()
+    ref16 = torch.softmax(s16 @ w.double().T + b.double(), -1) @ c
+    assert float((ed - ref16).abs().max()) <= 1e-4
+
+
 @pytest.mark.parametrize("n", [1, 2, 3, 1000, 1001, 56644, 57343, 57344, 57345, 65536, 65537, 300000])
 @pytest.mark.parametrize("q", [0.0, 0.5, 0.95, 1.0])
 def test_abs_diff_quantile(gpu_lib, pkg, n, q):
